@@ -1,0 +1,803 @@
+// Eviction boundary on the device: per-head selection (radix select over
+// 96-bit (score, position) keys), the shared target/leftover split, K/V/score
+// relocation, and the live-mode compaction of req_to_token.
+//
+// Ranking rule (R:376-397, C:114): protected positions are kept; the rest of
+// the budget goes to the highest float64 scores, exact ties keeping the newer
+// position. Positions are unique within a row, so the composite key
+// (ordered score bits, position) is unique and the top-k set is exact.
+#include "common.hpp"
+#include "host.hpp"
+
+namespace gse {
+
+constexpr int SEL_THREADS = 1024;
+constexpr int64_t MAX_POSITIONS = 491520;  // LDS position bitmap limit (60 KiB of words)
+
+// ------------------------------------------------------------------ helpers --
+
+GSE_DEVICE uint64_t splitmix_bits(int64_t seed, int64_t layer, int64_t head, int64_t pos) {
+  // R:366-373 / C:26-30, on wrapping 64-bit integers.
+  uint64_t x = uint64_t(pos) * 0x9E3779B97F4A7C15ull + uint64_t(layer) * 0xBF58476D1CE4E5B9ull +
+               uint64_t(head) * 0x94D049BB133111EBull + (uint64_t(seed) * 0xD1B54A32D192ED03ull + 0x632BE59BD9B4E019ull);
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  x = x ^ (x >> 31);
+  return x >> 11;
+}
+
+// Order-preserving map of a float64 to uint64 (larger double -> larger key).
+GSE_DEVICE uint64_t ordered_f64(double d) {
+  uint64_t u = __double_as_longlong(d);
+  return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
+}
+
+// Digit j (0 = most significant) of the 96-bit composite (key, pos).
+GSE_DEVICE uint32_t digit_of(uint64_t key, uint32_t pos, int j) {
+  return j < 8 ? uint32_t(key >> (56 - 8 * j)) & 0xffu : (pos >> (24 - 8 * (j - 8))) & 0xffu;
+}
+
+// Compare the first `fixed` digits of (key, pos) with the prefix: -1, 0 or +1.
+GSE_DEVICE int cmp_prefix(uint64_t key, uint32_t pos, uint64_t pk, uint32_t pp, int fixed) {
+  if (fixed <= 0) return 0;
+  if (fixed <= 8) {
+    const int sh = 64 - 8 * fixed;
+    const uint64_t a = sh >= 64 ? 0 : key >> sh, b = sh >= 64 ? 0 : pk >> sh;
+    return a < b ? -1 : (a > b ? 1 : 0);
+  }
+  if (key != pk) return key < pk ? -1 : 1;
+  const int sh = 32 - 8 * (fixed - 8);
+  const uint32_t a = sh >= 32 ? 0 : pos >> sh, b = sh >= 32 ? 0 : pp >> sh;
+  return a < b ? -1 : (a > b ? 1 : 0);
+}
+
+// Exclusive scan of one int per thread over the workgroup; returns the prefix, *total = sum.
+template <int THREADS>
+GSE_DEVICE int block_exclusive_scan(int v, int* tmp, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < THREADS / 64 ? tmp[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(w, o, 64);
+      if (lane >= o) w += y;
+    }
+    if (lane < THREADS / 64) tmp[64 + lane] = w;  // inclusive wave prefixes
+  }
+  __syncthreads();
+  const int before = wave ? tmp[64 + wave - 1] : 0;
+  *total = tmp[64 + THREADS / 64 - 1];
+  __syncthreads();
+  return before + x - v;
+}
+
+GSE_DEVICE int block_sum(int v, int* tmp) {
+  int total;
+  block_exclusive_scan<SEL_THREADS>(v, tmp, &total);
+  return total;
+}
+
+// ----------------------------------------------------------- column source --
+
+struct ColSrc {
+  // Boundary mode: pos(l, g, c) = c < count ? pos_old[(l*G + g)*pstride + c] : frontier + c - count.
+  const int32_t* pos_old;
+  int64_t pstride;
+  int64_t count, frontier;
+  // Public mode: pos[(l*G + g)*N + c] and score[(l*G + g)*N + c].
+  const int32_t* pos;
+  const double* score;
+  // Scores for the boundary policies.
+  int policy;
+  const float* table_scores;
+  int64_t ssl, ssg;
+  const int32_t* slots;
+  const double* random_scores;
+  int64_t seed;
+};
+
+struct SelArgs {
+  ColSrc src;
+  int layers, kv_heads;
+  int64_t n_cols, n, budget, prefix, recent, cursor;
+  int has_cursor, prefix_sliding, boundary_mode;
+  uint64_t* keys;     // [LG, N]
+  int32_t* posw;      // [LG, N]; protected stored as ~pos
+  int32_t* prot_count;
+  uint8_t* kept_mask;  // public mode: [LG, N]
+  // Boundary mode outputs.
+  int32_t* middle;    // [LG, budget] kept middle columns sorted by position
+  int32_t* prot_cols; // [budget] head (0, 0) protected columns sorted by position
+  int32_t* pos_new;   // [LG, budget]
+  int nwords;         // ceil(n / 32) position bitmap words
+};
+
+GSE_DEVICE bool is_protected(const SelArgs& a, int64_t p) {
+  return p < a.prefix || p >= a.n - a.recent || (a.has_cursor && p >= a.cursor);
+}
+
+// Rank of position p among the set bits of the LDS bitmap: block prefix + in-block popcounts.
+GSE_DEVICE int bitmap_rank(const uint32_t* words, const int* blockpre, int64_t p) {
+  const int w = int(p >> 5);
+  int r = blockpre[w >> 5];
+  for (int i = (w >> 5) << 5; i < w; ++i) r += __popc(words[i]);
+  return r + __popc(words[w] & ((1u << (p & 31)) - 1u));
+}
+
+// Exclusive prefix popcount of each 32-word group of the bitmap (one group per
+// thread; MAX_POSITIONS keeps the group count within one workgroup).
+GSE_DEVICE void bitmap_prefix(const uint32_t* words, int nwords, int* blockpre, int* tmp) {
+  const int ngroups = (nwords + 31) >> 5;
+  const int gi = threadIdx.x;
+  int c = 0;
+  if (gi < ngroups) {
+    const int lo = gi << 5, hi = min(nwords, lo + 32);
+    for (int i = lo; i < hi; ++i) c += __popc(words[i]);
+  }
+  int total;
+  const int ex = block_exclusive_scan<SEL_THREADS>(c, tmp, &total);
+  if (gi < ngroups) blockpre[gi] = ex;
+  __syncthreads();
+}
+
+// One workgroup per (full layer, KV head) row.
+__global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  int* tmp = reinterpret_cast<int*>(lds);             // 128 ints: scan scratch
+  int* hist = tmp + 128;                               // 256 bins
+  int* bcast = hist + 256;                             // 16 ints: broadcast
+  uint32_t* words = reinterpret_cast<uint32_t*>(bcast + 16);
+  int* blockpre = reinterpret_cast<int*>(words + a.nwords);
+
+  const int lg = blockIdx.x;
+  const int l = lg / a.kv_heads, g = lg % a.kv_heads;
+  const int64_t N = a.n_cols;
+  uint64_t* keys = a.keys + int64_t(lg) * N;
+  int32_t* posw = a.posw + int64_t(lg) * N;
+
+  // Phase 1: positions, protection and ordered score keys.
+  int nprot = 0;
+  for (int64_t c = threadIdx.x; c < N; c += SEL_THREADS) {
+    int64_t p;
+    double sc = 0.0;
+    if (a.boundary_mode) {
+      p = c < a.src.count ? int64_t(a.src.pos_old[int64_t(lg) * a.src.pstride + c]) : a.src.frontier + c - a.src.count;
+    } else {
+      p = a.src.pos[int64_t(lg) * N + c];
+    }
+    const bool prot = is_protected(a, p);
+    nprot += prot;
+    if (!prot && !a.prefix_sliding) {
+      if (!a.boundary_mode) {
+        sc = a.src.score[int64_t(lg) * N + c];
+      } else if (a.src.policy == GSE_POLICY_RESERVOIR) {
+        sc = double(splitmix_bits(a.src.seed, l, g, p)) / 9007199254740992.0;
+      } else if (a.src.policy == GSE_POLICY_RANDOM) {
+        sc = a.src.random_scores[int64_t(lg) * N + c];
+      } else {
+        sc = double(a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg + a.src.slots[c]]);
+      }
+    }
+    keys[c] = ordered_f64(sc);
+    posw[c] = prot ? ~int32_t(p) : int32_t(p);
+  }
+  const int P = block_sum(nprot, tmp);
+  if (threadIdx.x == 0) a.prot_count[lg] = P;
+  const int64_t M = N - P;
+  int64_t k = a.prefix_sliding ? 0 : a.budget - P;
+  if (k < 0) k = 0;  // deferred: keep nothing beyond the protected set
+  if (k > M) k = M;
+
+  // Phase 2: radix select of the k-th largest composite among unprotected columns.
+  uint64_t pk = 0;
+  uint32_t pp = 0;
+  int fixed = 0;
+  bool take_all = (k == M);
+  int64_t krem = k;
+  if (k > 0 && !take_all) {
+    for (int j = 0; j < 12; ++j) {
+      for (int i = threadIdx.x; i < 256; i += SEL_THREADS) hist[i] = 0;
+      __syncthreads();
+      for (int64_t c = threadIdx.x; c < N; c += SEL_THREADS) {
+        const int32_t pw = posw[c];
+        if (pw < 0) continue;
+        const uint64_t key = keys[c];
+        if (cmp_prefix(key, uint32_t(pw), pk, pp, j) != 0) continue;
+        atomicAdd(&hist[digit_of(key, uint32_t(pw), j)], 1);
+      }
+      __syncthreads();
+      if (threadIdx.x < 64) {
+        // Suffix sums over bins: lane owns bins [4*lane, 4*lane + 4).
+        const int lane = threadIdx.x;
+        const int c0 = hist[4 * lane], c1 = hist[4 * lane + 1], c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
+        int s = c0 + c1 + c2 + c3;
+        int suf = s;  // inclusive suffix over lanes >= lane
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_down(suf, o, 64);
+          if (lane + o < 64) suf += y;
+        }
+        const int above = suf - s;  // bins owned by higher lanes
+        // Find the bin b (descending) where the k-th largest falls.
+        const int cnt[4] = {c0, c1, c2, c3};
+        int acc = above;
+        for (int t = 3; t >= 0; --t) {
+          if (acc < krem && acc + cnt[t] >= krem) {
+            bcast[0] = 4 * lane + t;
+            bcast[1] = acc;
+            bcast[2] = cnt[t];
+          }
+          acc += cnt[t];
+        }
+      }
+      __syncthreads();
+      const uint32_t d = uint32_t(bcast[0]);
+      const int above = bcast[1], cntb = bcast[2];
+      __syncthreads();
+      if (j < 8)
+        pk |= uint64_t(d) << (56 - 8 * j);
+      else
+        pp |= d << (24 - 8 * (j - 8));
+      krem -= above;
+      fixed = j + 1;
+      if (cntb == krem) break;
+    }
+  }
+  // kept(c) = protected || (k > 0 && (take_all || first `fixed` digits >= prefix)).
+  auto kept_middle = [&](uint64_t key, int32_t pw) -> bool {
+    if (pw < 0 || k == 0) return false;
+    return take_all || cmp_prefix(key, uint32_t(pw), pk, pp, fixed) >= 0;
+  };
+
+  if (!a.boundary_mode) {
+    for (int64_t c = threadIdx.x; c < N; c += SEL_THREADS) {
+      const int32_t pw = posw[c];
+      a.kept_mask[int64_t(lg) * N + c] = uint8_t(pw < 0 || kept_middle(keys[c], pw));
+    }
+    return;
+  }
+  if (P > a.budget) return;  // deferred: outputs untouched
+
+  // Phase 3: kept middle columns ranked by position via the LDS bitmap.
+  for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < N; c += SEL_THREADS) {
+    const int32_t pw = posw[c];
+    if (kept_middle(keys[c], pw) && pw < a.n) atomicOr(&words[pw >> 5], 1u << (pw & 31));
+  }
+  __syncthreads();
+  bitmap_prefix(words, a.nwords, blockpre, tmp);
+  for (int64_t c = threadIdx.x; c < N; c += SEL_THREADS) {
+    const int32_t pw = posw[c];
+    if (!kept_middle(keys[c], pw) || pw >= a.n) continue;
+    const int r = bitmap_rank(words, blockpre, pw);
+    if (r < k) {
+      a.middle[int64_t(lg) * a.budget + r] = int32_t(c);
+      a.pos_new[int64_t(lg) * a.budget + P + r] = pw;
+    }
+  }
+  if (lg != 0) return;
+  // Head (0, 0): protected columns ranked by position.
+  __syncthreads();
+  for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < N; c += SEL_THREADS) {
+    const int32_t pw = posw[c];
+    if (pw < 0 && (~pw) < a.n) atomicOr(&words[(~pw) >> 5], 1u << ((~pw) & 31));
+  }
+  __syncthreads();
+  bitmap_prefix(words, a.nwords, blockpre, tmp);
+  for (int64_t c = threadIdx.x; c < N; c += SEL_THREADS) {
+    const int32_t pw = posw[c];
+    if (pw >= 0 || (~pw) >= a.n) continue;
+    const int r = bitmap_rank(words, blockpre, ~pw);
+    if (r < P) a.prot_cols[r] = int32_t(c);
+  }
+}
+
+// --------------------------------------------------------- boundary kernels --
+
+struct BndArgs {
+  int layers, kv_heads, head_dim;
+  int64_t N, n, budget;
+  int prefix_sliding;
+  const int32_t* table_in;  // read by prep only
+  int32_t* table;
+  int64_t table_stride;
+  const int32_t* r2t;
+  int64_t r2t_stride;
+  int32_t* frontier;
+  int32_t* count;
+  int row;
+  int64_t row_count, row_frontier;
+  const int32_t* pos_old;
+  int64_t pstride;
+  int32_t* slots;
+  int32_t* prot_count;
+  int32_t* middle;
+  int32_t* prot_cols;
+  int32_t* targets;
+  int32_t* pos_new;
+  int64_t* leftover;
+  gse_boundary_status* status;
+  int nwords_cols;
+  // relocation
+  void* const* k_pools;
+  void* const* v_pools;
+  int64_t kv_ss, kv_sh;
+  float* scores;
+  int64_t ssl, ssg;
+  uint16_t* scratch_kv;
+  float* scratch_sc;
+};
+
+// slots[c] = table[row, c] for c < count, else req_to_token[row, frontier + c - count] (R:428).
+__global__ void prep_slots_kernel(BndArgs a) {
+  const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= a.N) return;
+  a.slots[c] = c < a.row_count ? a.table[int64_t(a.row) * a.table_stride + c]
+                               : a.r2t[int64_t(a.row) * a.r2t_stride + a.row_frontier + c - a.row_count];
+}
+
+// Single workgroup: validate the per-head protected counts, split the
+// unprotected columns into targets and leftover, write the new table row.
+__global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  int* tmp = reinterpret_cast<int*>(lds);
+  int* bc = tmp + 128;
+  uint32_t* words = reinterpret_cast<uint32_t*>(bc + 16);
+  const int LG = a.layers * a.kv_heads;
+  if (threadIdx.x == 0) {
+    int mn = a.prot_count[0], mx = a.prot_count[0];
+    for (int i = 1; i < LG; ++i) {
+      mn = min(mn, a.prot_count[i]);
+      mx = max(mx, a.prot_count[i]);
+    }
+    const int P = a.prot_count[0];
+    int state = GSE_BOUNDARY_EVICTED;
+    if (mn != mx) state = GSE_BOUNDARY_ERR_HEADS;
+    else if (P > a.budget) state = GSE_BOUNDARY_DEFERRED;
+    const int64_t width = a.prefix_sliding ? 0 : a.budget - P;
+    bc[0] = state;
+    bc[1] = P;
+    bc[2] = int(width);
+    gse_boundary_status st;
+    st.state = state;
+    st.protected_count = P;
+    st.width = state == GSE_BOUNDARY_EVICTED ? int(width) : 0;
+    st.count = state == GSE_BOUNDARY_EVICTED ? int(P + width) : 0;
+    st.leftover = state == GSE_BOUNDARY_EVICTED ? int(a.N - P - width) : 0;
+    st.packed = 0;
+    st.min_protected = mn;
+    st.max_protected = mx;
+    *a.status = st;
+  }
+  __syncthreads();
+  if (bc[0] != GSE_BOUNDARY_EVICTED) return;
+  const int P = bc[1];
+  const int64_t width = bc[2];
+  for (int i = threadIdx.x; i < a.nwords_cols; i += SEL_THREADS) words[i] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < P; i += SEL_THREADS) {
+    const int c = a.prot_cols[i];
+    atomicOr(&words[c >> 5], 1u << (c & 31));
+  }
+  __syncthreads();
+  // Unprotected columns in column order: chunk of 32 columns per thread, scanned per pass.
+  int carry = 0;
+  for (int base = 0; base < a.nwords_cols; base += SEL_THREADS) {
+    const int w = base + threadIdx.x;
+    const uint32_t free_bits = w < a.nwords_cols ? ~words[w] : 0u;
+    const int64_t lo = int64_t(w) << 5;
+    uint32_t valid = 0;
+    if (w < a.nwords_cols) valid = lo + 32 <= a.N ? 0xffffffffu : ((1u << (a.N - lo)) - 1u);
+    const uint32_t bits = free_bits & valid;
+    int total;
+    const int ex = block_exclusive_scan<SEL_THREADS>(__popc(bits), tmp, &total);
+    int j = carry + ex;
+    for (int t = 0; t < 32; ++t) {
+      if (!(bits >> t & 1u)) continue;
+      const int32_t slot = a.slots[lo + t];
+      if (j < width)
+        a.targets[j] = slot;
+      else
+        a.leftover[j - width] = int64_t(slot);
+      ++j;
+    }
+    carry += total;
+  }
+  __syncthreads();
+  int32_t* trow = a.table + int64_t(a.row) * a.table_stride;
+  for (int i = threadIdx.x; i < P; i += SEL_THREADS) trow[i] = a.slots[a.prot_cols[i]];
+  for (int64_t j = threadIdx.x; j < width; j += SEL_THREADS) trow[P + j] = a.targets[j];
+  if (threadIdx.x == 0) {
+    a.count[a.row] = int32_t(P + width);
+    a.frontier[a.row] = int32_t(a.n);
+  }
+}
+
+// Gather (dir 0) every moved K/V/score row into scratch, or scatter (dir 1) it to its target.
+// Grid (ceil(width * chunks / 256), L*G); chunks = head_dim / 8 sixteen-byte pieces per row.
+template <int DIR>
+__global__ __launch_bounds__(256) void relocate_kernel(BndArgs a) {
+  const gse_boundary_status st = *a.status;
+  if (st.state != GSE_BOUNDARY_EVICTED) return;
+  const int64_t width = st.width;
+  const int lg = blockIdx.y;
+  const int l = lg / a.kv_heads, g = lg % a.kv_heads;
+  const int chunks = a.head_dim / 8;
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t j = t / chunks;
+  const int piece = int(t % chunks);
+  if (j >= width) return;
+  const int32_t col = a.middle[int64_t(lg) * a.budget + j];
+  const int64_t src = a.slots[col], dst = a.targets[j];
+  uint16_t* K = static_cast<uint16_t*>(a.k_pools[l]);
+  uint16_t* V = static_cast<uint16_t*>(a.v_pools[l]);
+  const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
+  uint16_t* sk = a.scratch_kv + ((int64_t(lg) * a.budget + j) * 2) * a.head_dim + 8 * piece;
+  uint16_t* sv = sk + a.head_dim;
+  float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
+  if (DIR == 0) {
+    *reinterpret_cast<uint4*>(sk) = *reinterpret_cast<const uint4*>(K + src * a.kv_ss + off);
+    *reinterpret_cast<uint4*>(sv) = *reinterpret_cast<const uint4*>(V + src * a.kv_ss + off);
+    if (piece == 0) a.scratch_sc[int64_t(lg) * a.budget + j] = srow[src];
+  } else {
+    *reinterpret_cast<uint4*>(K + dst * a.kv_ss + off) = *reinterpret_cast<const uint4*>(sk);
+    *reinterpret_cast<uint4*>(V + dst * a.kv_ss + off) = *reinterpret_cast<const uint4*>(sv);
+    if (piece == 0) srow[dst] = a.scratch_sc[int64_t(lg) * a.budget + j];
+  }
+}
+
+// pos_new[l, g, i] = pos(l, g, prot_cols[i]) for the protected prefix of every head row.
+__global__ __launch_bounds__(256) void protected_pos_kernel(BndArgs a) {
+  const gse_boundary_status st = *a.status;
+  if (st.state != GSE_BOUNDARY_EVICTED) return;
+  const int lg = blockIdx.x;
+  for (int i = threadIdx.x; i < st.protected_count; i += blockDim.x) {
+    const int64_t c = a.prot_cols[i];
+    const int64_t p = c < a.row_count ? int64_t(a.pos_old[int64_t(lg) * a.pstride + c]) : a.row_frontier + c - a.row_count;
+    a.pos_new[int64_t(lg) * a.budget + i] = int32_t(p);
+  }
+}
+
+// ---------------------------------------------------------- live compaction --
+
+struct LiveArgs {
+  float* scores;
+  int layers, kv_heads;
+  int64_t ssl, ssg;
+  const int32_t* table;
+  int64_t table_stride;
+  int32_t* r2t;
+  int64_t r2t_stride;
+  int row;
+  int64_t n, true_len;
+  const int64_t* leftover;
+  const void* swa;
+  int swa_dtype;
+  int64_t num_slots;
+  gse_boundary_status* status;
+  uint32_t* bitmap;  // ceil(num_slots / 32) words
+};
+
+__global__ void swa_guard_kernel(LiveArgs a) {
+  if (a.status->state != GSE_BOUNDARY_EVICTED) return;
+  const int64_t nl = a.status->leftover;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nl; i += int64_t(gridDim.x) * blockDim.x)
+    if (load_index_dyn(a.swa, a.swa_dtype, a.leftover[i]) != 0) atomicExch(&a.status->state, GSE_BOUNDARY_ERR_SWA);
+}
+
+__global__ void zero_leftover_kernel(LiveArgs a) {
+  if (a.status->state != GSE_BOUNDARY_EVICTED) return;
+  const int64_t nl = a.status->leftover;
+  const int64_t total = nl * a.layers * a.kv_heads;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t s = a.leftover[i % nl];
+    const int64_t lg = i / nl;
+    a.scores[(lg / a.kv_heads) * a.ssl + (lg % a.kv_heads) * a.ssg + s] = 0.f;
+  }
+}
+
+GSE_DEVICE uint32_t bitmap_load(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+GSE_DEVICE void bitmap_clear(uint32_t* p) { __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// Single workgroup: pack the owned slots that are not real at the start of the row (R:485-491).
+__global__ __launch_bounds__(SEL_THREADS) void repack_kernel(LiveArgs a) {
+  __shared__ int tmp[128 + 16];
+  if (a.status->state != GSE_BOUNDARY_EVICTED) return;
+  const int64_t cnt = a.status->count;
+  const int64_t nw = (a.num_slots + 31) >> 5;
+  for (int64_t i = threadIdx.x; i < nw; i += SEL_THREADS) bitmap_clear(&a.bitmap[i]);
+  __syncthreads();
+  int32_t* rrow = a.r2t + int64_t(a.row) * a.r2t_stride;
+  for (int64_t p = a.true_len + threadIdx.x; p < a.n; p += SEL_THREADS) {
+    const int64_t s = rrow[p];
+    if (s >= 0 && s < a.num_slots) atomicOr(&a.bitmap[s >> 5], 1u << (s & 31));
+  }
+  __syncthreads();
+  const int32_t* trow = a.table + int64_t(a.row) * a.table_stride;
+  // Count packed entries first; only write if they fit below true_len.
+  int mine = 0;
+  for (int64_t i = threadIdx.x; i < cnt; i += SEL_THREADS) {
+    const int64_t s = trow[i];
+    mine += !(bitmap_load(&a.bitmap[s >> 5]) >> (s & 31) & 1u);
+  }
+  const int packed = block_sum(mine, tmp);
+  if (threadIdx.x == 0) a.status->packed = packed;
+  if (packed > a.true_len) {
+    if (threadIdx.x == 0) a.status->state = GSE_BOUNDARY_ERR_PACKED;
+    return;
+  }
+  // In-order compaction: contiguous ranges per thread keep the table order.
+  const int64_t per = (cnt + SEL_THREADS - 1) / SEL_THREADS;
+  const int64_t lo = threadIdx.x * per, hi = min(cnt, lo + per);
+  int c = 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    const int64_t s = trow[i];
+    c += !(bitmap_load(&a.bitmap[s >> 5]) >> (s & 31) & 1u);
+  }
+  int total;
+  int j = block_exclusive_scan<SEL_THREADS>(c, tmp, &total);
+  // Rows [packed, true_len) become holes; [0, packed) get the packed slots.
+  for (int64_t i = packed + threadIdx.x; i < a.true_len; i += SEL_THREADS) rrow[i] = 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    const int64_t s = trow[i];
+    if (!(bitmap_load(&a.bitmap[s >> 5]) >> (s & 31) & 1u)) rrow[j++] = int32_t(s);
+  }
+}
+
+__global__ void reservoir_kernel(const void* pos, int pos_dtype, const int64_t* layer_ids, const int64_t* head_ids,
+                                 int layers, int kv_heads, int64_t n, int64_t seed, double* out) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n * layers * kv_heads) return;
+  const int64_t lg = i / n;
+  const int64_t l = lg / kv_heads, g = lg % kv_heads;
+  const int64_t lid = layer_ids ? layer_ids[l] : l;
+  const int64_t hid = head_ids ? head_ids[g] : g;
+  out[i] = double(splitmix_bits(seed, lid, hid, load_index_dyn(pos, pos_dtype, i))) / 9007199254740992.0;
+}
+
+}  // namespace gse
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+using namespace gse;
+
+namespace {
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+struct BndLayout {
+  int64_t slots, keys, posw, prot, middle, prot_cols, targets, skv, ssc, total;
+};
+
+BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t budget) {
+  const int64_t LG = int64_t(layers) * kv_heads;
+  BndLayout L;
+  int64_t o = 0;
+  L.slots = o; o += align256(N * 4);
+  L.keys = o; o += align256(LG * N * 8);
+  L.posw = o; o += align256(LG * N * 4);
+  L.prot = o; o += align256(LG * 4);
+  L.middle = o; o += align256(LG * budget * 4);
+  L.prot_cols = o; o += align256(budget * 4);
+  L.targets = o; o += align256(budget * 4);
+  L.skv = o; o += align256(LG * budget * 2 * head_dim * 2);
+  L.ssc = o; o += align256(LG * budget * 4);
+  L.total = o;
+  return L;
+}
+
+size_t select_lds_bytes(int nwords) {
+  const int ngroups = (nwords + 31) / 32;
+  return size_t(128 + 256 + 16) * 4 + size_t(nwords) * 4 + size_t(ngroups) * 4 + 16;
+}
+
+}  // namespace
+
+extern "C" int64_t gse_boundary_workspace_bytes(int layers, int kv_heads, int head_dim, int64_t n_cols, int64_t n,
+                                                int64_t budget) {
+  (void)n;
+  return bnd_layout(layers, kv_heads, head_dim, n_cols, budget).total;
+}
+
+extern "C" int64_t gse_boundary_live_workspace_bytes(int64_t num_slots) { return align256(((num_slots + 31) / 32) * 4); }
+
+extern "C" int gse_reservoir_scores(const void* pos, int pos_dtype, const int64_t* layer_ids, const int64_t* head_ids,
+                                    int layers, int kv_heads, int64_t n, int64_t seed, double* out,
+                                    gse_stream_t stream) {
+  if (layers < 0 || kv_heads < 0 || n < 0) return gse_fail(GSE_EINVAL, "reservoir: negative size");
+  const int64_t total = n * layers * kv_heads;
+  if (!total) return GSE_OK;
+  if (!pos || !out) return gse_fail(GSE_EINVAL, "reservoir: null pointer");
+  hipLaunchKernelGGL(reservoir_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), pos, pos_dtype, layer_ids, head_ids, layers, kv_heads, n,
+                     seed, out);
+  return gse_launch_check("reservoir");
+}
+
+extern "C" int gse_select_kept(const int32_t* pos, const double* score, int layers, int kv_heads, int64_t n_cols,
+                               int64_t n, int64_t budget, int64_t prefix, int64_t recent, int64_t cursor,
+                               int has_cursor, int prefix_sliding, uint8_t* kept_mask, int32_t* prot_count,
+                               void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
+  if (layers <= 0 || kv_heads <= 0 || n_cols < 0 || n_cols >= (int64_t(1) << 31))
+    return gse_fail(GSE_EINVAL, "select: bad sizes");
+  if (!pos || !kept_mask || !prot_count || (!score && !prefix_sliding)) return gse_fail(GSE_EINVAL, "select: null");
+  const int64_t LG = int64_t(layers) * kv_heads;
+  const int64_t need = align256(LG * n_cols * 8) + align256(LG * n_cols * 4);
+  if (workspace_bytes < need) return gse_fail(GSE_EWORKSPACE, "select: workspace too small");
+  SelArgs a = {};
+  a.src.pos = pos;
+  a.src.score = score;
+  a.layers = layers;
+  a.kv_heads = kv_heads;
+  a.n_cols = n_cols;
+  a.n = n;
+  a.budget = budget;
+  a.prefix = prefix;
+  a.recent = recent;
+  a.cursor = cursor;
+  a.has_cursor = has_cursor;
+  a.prefix_sliding = prefix_sliding;
+  a.boundary_mode = 0;
+  a.keys = static_cast<uint64_t*>(workspace);
+  a.posw = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(LG * n_cols * 8));
+  a.prot_count = prot_count;
+  a.kept_mask = kept_mask;
+  a.nwords = 0;
+  hipLaunchKernelGGL(select_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), select_lds_bytes(0),
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return gse_launch_check("select");
+}
+
+extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s,
+                            int64_t kv_stride_h, int kv_heads, int head_dim, float* scores, int64_t scores_stride_l,
+                            int64_t scores_stride_g, int32_t* table, int64_t table_stride,
+                            const int32_t* req_to_token, int64_t r2t_stride, int32_t* frontier, int32_t* count, int row,
+                            int64_t row_count, int64_t row_frontier, const int32_t* pos_old, int64_t pos_old_stride,
+                            int64_t n, int64_t budget, int64_t prefix, int64_t recent, int64_t cursor, int has_cursor,
+                            int policy, int64_t seed, const double* random_scores, int32_t* pos_new,
+                            int64_t* leftover, gse_boundary_status* status, void* workspace, int64_t workspace_bytes,
+                            gse_stream_t stream) {
+  const int64_t N = row_count + n - row_frontier;
+  if (layers <= 0 || kv_heads <= 0 || budget <= 0 || N <= budget)
+    return gse_fail(GSE_EINVAL, "boundary: needs layers, kv_heads, budget > 0 and N > budget");
+  if (head_dim % 8 || head_dim <= 0 || kv_stride_h % 8 || kv_stride_s % 8)
+    return gse_fail(GSE_ESHAPE, "boundary: head_dim and K/V strides must be multiples of 8");
+  if (n > MAX_POSITIONS || N >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "boundary: logical length too large");
+  if (row_count > 0 && !pos_old) return gse_fail(GSE_EINVAL, "boundary: pos_old needed when count > 0");
+  if (policy < GSE_POLICY_HEAD_SUM || policy > GSE_POLICY_PREFIX_SLIDING)
+    return gse_fail(GSE_EINVAL, "boundary: unknown policy");
+  if (policy == GSE_POLICY_RANDOM && !random_scores) return gse_fail(GSE_EINVAL, "boundary: random_2048 needs scores");
+  if (!k_pools || !v_pools || !scores || !table || !req_to_token || !frontier || !count || !pos_new || !leftover ||
+      !status)
+    return gse_fail(GSE_EINVAL, "boundary: null pointer");
+  const BndLayout L = bnd_layout(layers, kv_heads, head_dim, N, budget);
+  if (workspace_bytes < L.total) return gse_fail(GSE_EWORKSPACE, "boundary: workspace too small");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int LG = layers * kv_heads;
+
+  BndArgs b = {};
+  b.layers = layers;
+  b.kv_heads = kv_heads;
+  b.head_dim = head_dim;
+  b.N = N;
+  b.n = n;
+  b.budget = budget;
+  b.prefix_sliding = policy == GSE_POLICY_PREFIX_SLIDING;
+  b.table = table;
+  b.table_stride = table_stride;
+  b.r2t = req_to_token;
+  b.r2t_stride = r2t_stride;
+  b.frontier = frontier;
+  b.count = count;
+  b.row = row;
+  b.row_count = row_count;
+  b.row_frontier = row_frontier;
+  b.pos_old = pos_old;
+  b.pstride = pos_old_stride;
+  b.slots = reinterpret_cast<int32_t*>(ws + L.slots);
+  b.prot_count = reinterpret_cast<int32_t*>(ws + L.prot);
+  b.middle = reinterpret_cast<int32_t*>(ws + L.middle);
+  b.prot_cols = reinterpret_cast<int32_t*>(ws + L.prot_cols);
+  b.targets = reinterpret_cast<int32_t*>(ws + L.targets);
+  b.pos_new = pos_new;
+  b.leftover = leftover;
+  b.status = status;
+  b.nwords_cols = int((N + 31) / 32);
+  b.k_pools = k_pools;
+  b.v_pools = v_pools;
+  b.kv_ss = kv_stride_s;
+  b.kv_sh = kv_stride_h;
+  b.scores = scores;
+  b.ssl = scores_stride_l;
+  b.ssg = scores_stride_g;
+  b.scratch_kv = reinterpret_cast<uint16_t*>(ws + L.skv);
+  b.scratch_sc = reinterpret_cast<float*>(ws + L.ssc);
+
+  hipLaunchKernelGGL(prep_slots_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, s, b);
+  if (int rc = gse_launch_check("boundary prep")) return rc;
+
+  SelArgs a = {};
+  a.src.pos_old = pos_old;
+  a.src.pstride = pos_old_stride;
+  a.src.count = row_count;
+  a.src.frontier = row_frontier;
+  a.src.policy = policy;
+  a.src.table_scores = scores;
+  a.src.ssl = scores_stride_l;
+  a.src.ssg = scores_stride_g;
+  a.src.slots = b.slots;
+  a.src.random_scores = random_scores;
+  a.src.seed = seed;
+  a.layers = layers;
+  a.kv_heads = kv_heads;
+  a.n_cols = N;
+  a.n = n;
+  a.budget = budget;
+  a.prefix = prefix;
+  a.recent = recent;
+  a.cursor = cursor;
+  a.has_cursor = has_cursor;
+  a.prefix_sliding = b.prefix_sliding;
+  a.boundary_mode = 1;
+  a.keys = reinterpret_cast<uint64_t*>(ws + L.keys);
+  a.posw = reinterpret_cast<int32_t*>(ws + L.posw);
+  a.prot_count = b.prot_count;
+  a.middle = b.middle;
+  a.prot_cols = b.prot_cols;
+  a.pos_new = pos_new;
+  a.nwords = int((n + 31) / 32);
+  hipLaunchKernelGGL(select_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), select_lds_bytes(a.nwords), s, a);
+  if (int rc = gse_launch_check("boundary select")) return rc;
+
+  const size_t col_lds = size_t(128 + 16) * 4 + size_t(b.nwords_cols) * 4 + 16;
+  hipLaunchKernelGGL(columns_kernel, dim3(1), dim3(SEL_THREADS), col_lds, s, b);
+  if (int rc = gse_launch_check("boundary columns")) return rc;
+
+  const int chunks = head_dim / 8;
+  const dim3 rgrid(unsigned((budget * chunks + 255) / 256), unsigned(LG));
+  hipLaunchKernelGGL(relocate_kernel<0>, rgrid, dim3(256), 0, s, b);
+  if (int rc = gse_launch_check("boundary gather")) return rc;
+  hipLaunchKernelGGL(relocate_kernel<1>, rgrid, dim3(256), 0, s, b);
+  if (int rc = gse_launch_check("boundary scatter")) return rc;
+  hipLaunchKernelGGL(protected_pos_kernel, dim3(unsigned(LG)), dim3(256), 0, s, b);
+  return gse_launch_check("boundary protected pos");
+}
+
+extern "C" int gse_boundary_live(float* scores, int layers, int64_t scores_stride_l, int kv_heads,
+                                 int64_t scores_stride_g, const int32_t* table, int64_t table_stride,
+                                 int32_t* req_to_token, int64_t r2t_stride, int row, int64_t n, int64_t true_len,
+                                 const int64_t* leftover, const void* swa_mapping, int swa_dtype, int64_t num_slots,
+                                 gse_boundary_status* status, void* workspace, int64_t workspace_bytes,
+                                 gse_stream_t stream) {
+  if (!scores || !table || !req_to_token || !leftover || !status || !workspace)
+    return gse_fail(GSE_EINVAL, "boundary_live: null pointer");
+  if (num_slots <= 0 || true_len < 0 || true_len > n) return gse_fail(GSE_EINVAL, "boundary_live: bad sizes");
+  if (workspace_bytes < gse_boundary_live_workspace_bytes(num_slots))
+    return gse_fail(GSE_EWORKSPACE, "boundary_live: workspace too small");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  LiveArgs a = {scores, layers, kv_heads, scores_stride_l, scores_stride_g, table, table_stride, req_to_token,
+                r2t_stride, row, n, true_len, leftover, swa_mapping, swa_dtype, num_slots, status,
+                static_cast<uint32_t*>(workspace)};
+  // The kernels read the leftover count from *status; grid-stride loops cover any count.
+  if (swa_mapping) {
+    hipLaunchKernelGGL(swa_guard_kernel, dim3(64), dim3(256), 0, s, a);
+    if (int rc = gse_launch_check("swa guard")) return rc;
+  }
+  hipLaunchKernelGGL(zero_leftover_kernel, dim3(256), dim3(256), 0, s, a);
+  if (int rc = gse_launch_check("zero leftover")) return rc;
+  hipLaunchKernelGGL(repack_kernel, dim3(1), dim3(SEL_THREADS), 0, s, a);
+  return gse_launch_check("repack");
+}

@@ -1,0 +1,115 @@
+"""ctypes binding of libgstar_evict.so, the C ABI declared in include/gstar_evict.h.
+
+The library is loaded once from this package's directory. There is no
+fallback: if it is missing or a call fails, the caller gets an exception.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libgstar_evict.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+GSE_OK = 0
+I32, I64 = 0, 1
+F32, BF16 = 0, 1
+SCORE_NONE, SCORE_EAGER, SCORE_LAG = 0, 1, 2
+POLICY_IDS = {"head_sum_2048": 1, "head_max_sum_2048": 2, "random_2048": 3,
+              "random_reservoir_2048": 4, "prefix_sliding_2048": 5}
+BOUNDARY_EVICTED, BOUNDARY_DEFERRED, BOUNDARY_ERR_HEADS, BOUNDARY_ERR_SWA, BOUNDARY_ERR_PACKED = 0, 2, 3, 4, 5
+
+_p, _i, _l, _f, _d = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double
+
+# name -> (restype, argtypes); mirrors include/gstar_evict.h.
+SIGNATURES = {
+    "gse_version": (_i, []),
+    "gse_last_error": (ctypes.c_char_p, []),
+    "gse_fill": (_i, [_p, _l, _p, _l, _p, _i, _p, _i, _p, _p, _i, _p, _p, _i, _p]),
+    "gse_zero_slots": (_i, [_p, _i, _l, _i, _l, _p, _i, _l, _p]),
+    "gse_decode_workspace_bytes": (_l, [_i, _i, _i, _i]),
+    "gse_decode": (_i, [_p, _l, _l, _p, _p, _l, _l, _p, _p, _i, _p, _i, _p, _p, _i, _p, _l, _p, _l, _l, _p,
+                        _p, _p, _p, _i, _i, _i, _i, _f, _i, _i, _i, _p, _l, _p]),
+    "gse_decode_flush": (_i, [_p, _l, _l, _p, _l, _p, _l, _l, _p, _p, _p, _p, _i, _i, _p, _l, _p, _p, _p,
+                              _i, _i, _i, _f, _i, _i, _p]),
+    "gse_decode_scores_from_lse": (_i, [_p, _l, _l, _p, _l, _l, _p, _p, _i, _p, _l, _l, _p, _i, _i, _p, _i,
+                                        _p, _p, _i, _p, _l, _i, _i, _i, _i, _f, _i, _i, _p, _l, _p]),
+    "gse_reservoir_scores": (_i, [_p, _i, _p, _p, _i, _i, _l, _l, _p, _p]),
+    "gse_select_kept": (_i, [_p, _p, _i, _i, _l, _l, _l, _l, _l, _l, _i, _i, _p, _p, _p, _l, _p]),
+    "gse_boundary_workspace_bytes": (_l, [_i, _i, _i, _l, _l, _l]),
+    "gse_boundary": (_i, [_p, _p, _i, _l, _l, _i, _i, _p, _l, _l, _p, _l, _p, _l, _p, _p, _i, _l, _l, _p, _l,
+                          _l, _l, _l, _l, _l, _i, _i, _l, _p, _p, _p, _p, _p, _l, _p]),
+    "gse_boundary_live_workspace_bytes": (_l, [_l]),
+    "gse_boundary_live": (_i, [_p, _i, _l, _i, _l, _p, _l, _p, _l, _i, _l, _l, _p, _p, _i, _l, _p, _p, _l, _p]),
+    "gse_prefill_workspace_bytes": (_l, [_l, _i]),
+    "gse_prefill_scores": (_i, [_p, _l, _l, _l, _p, _l, _l, _p, _i, _l, _l, _p, _i, _i, _p, _l, _i, _i, _i,
+                                _f, _p, _l, _p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise NativeError(f"{LIB_PATH} is missing: build it with `python cache-eviction_amd/build.py`")
+                handle = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(handle, name, None)
+                    if fn is not None:
+                        fn.restype, fn.argtypes = res, args
+                _lib = handle
+    return _lib
+
+
+def call(name, *args):
+    """Call an entry point; a non-zero status raises NativeError with the library's message."""
+    fn = getattr(lib(), name, None)
+    if fn is None:
+        raise NativeError(f"{LIB_NAME} does not export {name}")
+    rc = fn(*args)
+    if rc != GSE_OK:
+        raise NativeError(f"{name} failed ({rc}): {lib().gse_last_error().decode()}")
+    return rc
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def idx_code(t):
+    if t.dtype == torch.int64:
+        return I64
+    if t.dtype == torch.int32:
+        return I32
+    raise TypeError(f"index tensors must be int32 or int64, got {t.dtype}")
+
+
+def float_code(t):
+    if t.dtype == torch.bfloat16:
+        return BF16
+    if t.dtype == torch.float32:
+        return F32
+    raise TypeError(f"expected float32 or bfloat16, got {t.dtype}")
+
+
+def stream(device=None):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def exported_symbols():
+    """Names declared in the header that the built library exports."""
+    handle = ctypes.CDLL(LIB_PATH)
+    return [n for n in SIGNATURES if hasattr(handle, n)]

@@ -1,0 +1,254 @@
+/*
+ * gstar_evict — C ABI of the MI355X (gfx950) KV-cache eviction hot path.
+ *
+ * Every entry point takes caller-owned device buffers as plain pointers with
+ * element strides, sizes as integers, and the HIP stream to launch on as the
+ * last argument. Entry points return GSE_OK or an error code; the message of
+ * the last error on the calling thread is available from gse_last_error().
+ * Kernels never allocate; buffers the kernels need beyond inputs and outputs
+ * come in through a caller-provided workspace.
+ *
+ * Reference paths below are relative to the tonghuikang/cache-eviction
+ * repository: R = code/cache_eviction/sglang_evict_runtime.py,
+ * C = code/cache_eviction/core.py, T = code/tests/test_sglang_evict.py.
+ *
+ * Layouts (the reference's, R:89-110):
+ *   K/V pool of one layer   bf16 [slots, kv_heads, head_dim], head_dim contiguous
+ *   scores                  fp32 [full layers, kv_heads, slots] (any strides)
+ *   table / req_to_token    int32 [rows, width]
+ *   frontier / count / mode int32 [rows]
+ *   pos (per row)           int32 [full layers, kv_heads, count]
+ */
+#ifndef GSTAR_EVICT_H
+#define GSTAR_EVICT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* gse_stream_t; /* hipStream_t */
+
+enum { GSE_OK = 0, GSE_EINVAL = 1, GSE_ESHAPE = 2, GSE_ELAUNCH = 3, GSE_EWORKSPACE = 4 };
+enum { GSE_I32 = 0, GSE_I64 = 1 };  /* dtype codes of index arrays */
+enum { GSE_F32 = 0, GSE_BF16 = 1 }; /* dtype codes of float arrays */
+
+/* Policy ids of the boundary selector (names of R:45-46). */
+enum {
+  GSE_POLICY_HEAD_SUM = 1,         /* head_sum_2048: scores gathered from the score table */
+  GSE_POLICY_HEAD_MAX_SUM = 2,     /* head_max_sum_2048: same gather                   */
+  GSE_POLICY_RANDOM = 3,           /* random_2048: caller-drawn float64 scores          */
+  GSE_POLICY_RESERVOIR = 4,        /* random_reservoir_2048: splitmix64 in-kernel       */
+  GSE_POLICY_PREFIX_SLIDING = 5    /* prefix_sliding_2048: protected set only           */
+};
+
+/* Decode score modes of gse_decode. */
+enum {
+  GSE_SCORE_NONE = 0,  /* attention only                                               */
+  GSE_SCORE_EAGER = 1, /* this step's scores are added before the call returns          */
+  GSE_SCORE_LAG = 2    /* the previous step's scores are added while K streams for this  */
+                       /* step; this step's are left pending (see gse_decode_flush)      */
+};
+
+/* Boundary outcome written to device memory by gse_boundary. */
+enum {
+  GSE_BOUNDARY_EVICTED = 0,
+  GSE_BOUNDARY_DEFERRED = 2,       /* protected count > budget (R:390-391, R:438-441)       */
+  GSE_BOUNDARY_ERR_HEADS = 3,      /* heads protect different counts (R:388-389)             */
+  GSE_BOUNDARY_ERR_SWA = 4,        /* a leftover slot still holds a sliding-window entry (R:477-479) */
+  GSE_BOUNDARY_ERR_PACKED = 5      /* packed ownership overlaps the sliding-window region (R:487-489) */
+};
+
+typedef struct {
+  int32_t state;            /* GSE_BOUNDARY_*                                   */
+  int32_t protected_count;  /* protected columns of head (0, 0)                 */
+  int32_t width;            /* kept middle columns per head                     */
+  int32_t count;            /* new table length = protected_count + width       */
+  int32_t leftover;         /* slots handed back (candidates beyond width)      */
+  int32_t packed;           /* owned slots packed at the start of req_to_token  */
+  int32_t min_protected;    /* smallest per-head protected count                */
+  int32_t max_protected;    /* largest per-head protected count                 */
+} gse_boundary_status;
+
+/* Library version (major * 10000 + minor * 100 + patch) and last error text. */
+int gse_version(void);
+const char* gse_last_error(void);
+
+/*
+ * fill — full-layer CSR of resident slots. Replaces R:136-152 (`fill`, with
+ * SGLang's create_flashinfer_kv_indices_triton called twice, R:147-151):
+ *   kv_indptr[b+1] = sum_{i<=b} (seq_lens[i] - frontier[rows[i]] + count[rows[i]])
+ *   kv_indices     = table[row, :count] ++ req_to_token[row, frontier:seq_len]   per b
+ * Fixed grid (bs workgroups), no host reads: capturable in a HIP graph.
+ */
+int gse_fill(const int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
+             const void* rows, int rows_dtype, const void* seq_lens, int lens_dtype,
+             const int32_t* frontier, const int32_t* count, int bs,
+             int32_t* kv_indptr, void* kv_indices, int indices_dtype, gse_stream_t stream);
+
+/*
+ * zero_slots — scores[l, g, slots[i]] = 0 for every full layer l and KV head g.
+ * Replaces R:211-212 / R:293-294 (`st.scores.index_fill_(2, out_cache_loc, 0.0)`).
+ */
+int gse_zero_slots(float* scores, int layers, int64_t layer_stride, int kv_heads, int64_t head_stride,
+                   const void* slots, int slots_dtype, int64_t n, gse_stream_t stream);
+
+/* Workspace bytes gse_decode / gse_decode_scores_from_lse need for bs sequences and max_splits splits. */
+int64_t gse_decode_workspace_bytes(int bs, int max_splits, int q_heads, int head_dim);
+
+/*
+ * decode — one full-attention layer's decode step: split-KV attention with the
+ * learned sink folded into the softmax normaliser, fused with the per-KV-head
+ * H2O score update. Replaces SGLang's decode_attention_fwd (the attention of
+ * R:203-224's caller, O:35-41) together with `_decode_scores` / `after_decode`
+ * (R:155-224).
+ *   o[b, h]      = sum_s softmax([q_h.k_s*scale, sink_h])_s v_s  (sink column dropped)
+ *   norm_out[b,h] = log(exp(sink_h) + sum_s exp(q_h.k_s*scale))
+ *   scores[g, slot_s] += sum_{h in g} p_hs   (mode 1)  or  max_{h in g} p_hs  (mode 2)
+ * where mode = mode_by_row[rows[b]]; rows whose mode is not 1 or 2 get no score.
+ * score_mode selects GSE_SCORE_NONE / _EAGER / _LAG. In LAG mode the kernel
+ * adds the scores of the query left pending in (pend_q, pend_norm, pend_len) for
+ * this layer by the previous call while it streams K for this call, then leaves
+ * this call's query pending; the pending rows' slot lists must be prefixes of
+ * this call's lists (true between boundaries). Shapes: q_heads = 8 * kv_heads,
+ * kv_heads <= 8, head_dim = 64. Fixed grid (max_splits x bs): capturable.
+ */
+int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+               const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
+               const int32_t* kv_indptr, const void* kv_indices, int indices_dtype,
+               const void* sinks, int sinks_dtype, const int32_t* mode_by_row, const void* rows, int rows_dtype,
+               float* scores, int64_t scores_stride_g,
+               void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
+               void* pend_q, float* pend_norm, int32_t* pend_len,
+               int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int chunk, int max_splits,
+               int score_mode, void* workspace, int64_t workspace_bytes, gse_stream_t stream);
+
+/*
+ * decode_flush — add the pending (LAG mode) scores of the listed rows of one
+ * layer and clear them. The slot list of a pending row is rebuilt from the
+ * eviction state as in `fill`: table[row, :count] ++ req_to_token[row, frontier:],
+ * truncated to pend_len[row]. No reference counterpart: the reference adds
+ * scores eagerly (R:218-224); this restores the same scores before they are read.
+ */
+int gse_decode_flush(const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_h,
+                     const int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
+                     int64_t r2t_width, const int32_t* frontier, const int32_t* count, const int32_t* mode_by_row,
+                     const void* rows, int rows_dtype, int n_rows,
+                     float* scores, int64_t scores_stride_g,
+                     void* pend_q, float* pend_norm, int32_t* pend_len,
+                     int q_heads, int kv_heads, int head_dim, float sm_scale, int chunk, int max_splits,
+                     gse_stream_t stream);
+
+/*
+ * decode_scores_from_lse — the reference's score update given an external
+ * decode kernel's split log-sum-exps. Replaces `_decode_scores` + `after_decode`
+ * (R:155-224) exactly: the normaliser is rebuilt from attn_lse [bs, q_heads,
+ * max_kv_splits] (strides in elements) over the valid splits of SGLang's layout
+ * per = cdiv(cdiv(len, num_kv_splits[b]), min_block_kv) * min_block_kv, started
+ * at (sink, 1) (R:180-188), then every resident key's probability is added.
+ */
+int gse_decode_scores_from_lse(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                               const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_h,
+                               const int32_t* kv_indptr, const void* kv_indices, int indices_dtype,
+                               const float* attn_lse, int64_t lse_stride_b, int64_t lse_stride_h,
+                               const int32_t* num_kv_splits, int max_kv_splits, int min_block_kv,
+                               const void* sinks, int sinks_dtype, const int32_t* mode_by_row,
+                               const void* rows, int rows_dtype, float* scores, int64_t scores_stride_g,
+                               int bs, int q_heads, int kv_heads, int head_dim, float sm_scale,
+                               int chunk, int max_splits, void* workspace, int64_t workspace_bytes,
+                               gse_stream_t stream);
+
+/*
+ * reservoir_scores — out[l, g, i] = (splitmix64 of (seed, layer_ids[l], head_ids[g], pos[l, g, i])) >> 11, / 2^53.
+ * Replaces R:358-373 (and C:23-30). pos is int32 or int64 [L, G, N] contiguous;
+ * null layer_ids / head_ids mean 0..L-1 / 0..G-1.
+ */
+int gse_reservoir_scores(const void* pos, int pos_dtype, const int64_t* layer_ids, const int64_t* head_ids,
+                         int layers, int kv_heads, int64_t n, int64_t seed, double* out, gse_stream_t stream);
+
+/*
+ * select_kept — per (layer, KV head) row of pos [L, G, N] (int32) and float64
+ * keys (score [L, G, N]; protected entries are ranked first), mark the kept
+ * columns: protected ∪ top-(budget - protected) by (score desc, position desc).
+ * Replaces the ranking of `choose` (R:376-397); kept_mask is uint8 [L, G, N],
+ * prot_count int32 [L, G]. prefix_sliding keeps only the protected set.
+ */
+int gse_select_kept(const int32_t* pos, const double* score, int layers, int kv_heads, int64_t n_cols,
+                    int64_t n, int64_t budget, int64_t prefix, int64_t recent, int64_t cursor, int has_cursor,
+                    int prefix_sliding, uint8_t* kept_mask, int32_t* prot_count, void* workspace,
+                    int64_t workspace_bytes, gse_stream_t stream);
+
+/* Workspace bytes gse_select_kept and gse_boundary need (n_cols = N columns, n = logical length). */
+int64_t gse_boundary_workspace_bytes(int layers, int kv_heads, int head_dim, int64_t n_cols, int64_t n,
+                                     int64_t budget);
+
+/*
+ * boundary — ranking half of one row's eviction boundary at logical length n.
+ * Replaces `choose`/`_scores` (R:376-412) and R:415-475 of `_boundary`:
+ *   slots  = table[row, :count] ++ req_to_token[row, frontier:n]            (R:428)
+ *   pos    = pos_old[l, g, :count] ++ arange(frontier, n)                    (R:429-431)
+ *   keep   = protected ∪ top-k by (score desc, position desc) per head       (R:376-397)
+ *   middle = each head's kept non-protected columns sorted by position       (R:444-446)
+ *   targets/leftover = non-protected slots in column order split at width    (R:447-451)
+ *   K, V, score of (middle[l,g,j], g) -> (targets[j], g) for every full layer (R:455-463)
+ *   table[row] = slots[protected cols] ++ targets; count; frontier = n        (R:468-473)
+ * k_pools / v_pools are device arrays of `layers` device pointers. pos_old rows
+ * are pos_old_stride elements apart. Writes pos_new [L, G, budget] (first
+ * `count` columns valid), leftover slots (int64, N - count of them) and
+ * *status. Deferred or invalid boundaries (status.state != EVICTED) change no
+ * state. Call only when N = row_count + n - row_frontier > budget (R:433-435).
+ */
+int gse_boundary(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                 int kv_heads, int head_dim, float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                 int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
+                 int32_t* frontier, int32_t* count, int row, int64_t row_count, int64_t row_frontier,
+                 const int32_t* pos_old, int64_t pos_old_stride, int64_t n, int64_t budget, int64_t prefix,
+                 int64_t recent, int64_t cursor, int has_cursor, int policy, int64_t seed,
+                 const double* random_scores, int32_t* pos_new, int64_t* leftover, gse_boundary_status* status,
+                 void* workspace, int64_t workspace_bytes, gse_stream_t stream);
+
+/* Workspace bytes gse_boundary_live needs for a pool of num_slots slots. */
+int64_t gse_boundary_live_workspace_bytes(int64_t num_slots);
+
+/*
+ * boundary_live — compaction half of a live boundary (R:476-491), after
+ * gse_boundary reported EVICTED in *status:
+ *   ERR_SWA if swa_mapping[leftover[i]] != 0 for any leftover slot (R:477-479), else
+ *   scores[:, :, leftover] = 0                                            (R:481)
+ *   true = min(n - recent, cursor or n); real = req_to_token[row, true:n]  (R:485-486)
+ *   packed = table[row, :count] entries not in real, in order             (R:487)
+ *   ERR_PACKED if len(packed) > true (R:488-489), else
+ *   req_to_token[row, :true] = 0; req_to_token[row, :len(packed)] = packed (R:490-491)
+ * swa_mapping (int32/int64 [num_slots]) may be null. The caller frees the
+ * leftover slots (status.leftover of them) once the stream completes.
+ */
+int gse_boundary_live(float* scores, int layers, int64_t scores_stride_l, int kv_heads, int64_t scores_stride_g,
+                      const int32_t* table, int64_t table_stride, int32_t* req_to_token, int64_t r2t_stride,
+                      int row, int64_t n, int64_t true_len, const int64_t* leftover, const void* swa_mapping,
+                      int swa_dtype, int64_t num_slots, gse_boundary_status* status, void* workspace,
+                      int64_t workspace_bytes, gse_stream_t stream);
+
+/*
+ * prefill_scores — one extend chunk's exact per-KV-head column sums, added to
+ * the score table (R:314-340, `_probabilities` + `_prefill_scores`):
+ *   p[h, i, k] = exp(q_i,h . k_k * scale - logaddexp(logsumexp_k'(...), sink_h)),  k <= prefix_len + i
+ *   scores[g, slots[k]] += sum_i (sum_{h in g} | max_{h in g}) p[h, i, k]
+ * q [count, q_heads, head_dim] bf16, keys gathered through slots (int64 or
+ * int32, prefix slots then the chunk's own) from the pool. head_dim = 64,
+ * q_heads = 8 * kv_heads. MFMA 16x16x32 bf16 tiles, two passes (row
+ * log-sum-exp, then column sums). Needs workspace for the row normalisers.
+ */
+int64_t gse_prefill_workspace_bytes(int64_t count, int q_heads);
+int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t count,
+                       const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_h,
+                       const void* slots, int slots_dtype, int64_t total, int64_t prefix_len,
+                       const void* sinks, int sinks_dtype, int mode, float* scores, int64_t scores_stride_g,
+                       int q_heads, int kv_heads, int head_dim, float sm_scale,
+                       void* workspace, int64_t workspace_bytes, gse_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSTAR_EVICT_H */

@@ -1,0 +1,65 @@
+"""The C ABI: the library builds, loads, and exports every entry point the header declares
+with the argument list the Python binding uses (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from gstar_evict import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gstar_evict.h")
+
+CTYPES = {"void*": ctypes.c_void_p, "int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float,
+          "double": ctypes.c_double, "gse_stream_t": ctypes.c_void_p, "char*": ctypes.c_char_p}
+
+
+def header_prototypes():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    protos = {}
+    for m in re.finditer(r"^\s*(int64_t|int|const char\*)\s+(gse_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+        ret, name, args = m.group(1), m.group(2), m.group(3).strip()
+        kinds = []
+        if args and args != "void":
+            for arg in args.split(","):
+                arg = " ".join(arg.replace("const", " ").split())
+                if "*" in arg:
+                    kinds.append("void*")
+                else:
+                    kinds.append(arg.rsplit(" ", 1)[0])
+        protos[name] = (ret.replace("const ", ""), kinds)
+    return protos
+
+
+def test_header_and_binding_agree():
+    protos = header_prototypes()
+    assert len(protos) >= 15
+    assert set(protos) == set(_native.SIGNATURES), set(protos) ^ set(_native.SIGNATURES)
+    for name, (ret, kinds) in protos.items():
+        res, args = _native.SIGNATURES[name]
+        want_ret = {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "char*": ctypes.c_char_p}[ret]
+        assert res is want_ret, name
+        assert [CTYPES[k] for k in kinds] == list(args), name
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    handle = ctypes.CDLL(_native.LIB_PATH)
+    missing = [n for n in header_prototypes() if not hasattr(handle, n)]
+    assert not missing, missing
+    assert _native.lib().gse_version() >= 100
+
+
+def test_entry_points_reject_bad_arguments_without_a_gpu():
+    """Argument validation runs on the host before any launch."""
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    lib = _native.lib()
+    rc = lib.gse_decode(None, 0, 0, None, None, 0, 0, None, None, 0, None, 0, None, None, 0, None, 0, None, 0, 0,
+                        None, None, None, None, 4, 64, 8, 128, 0.125, 512, 8, 0, None, 0, None)
+    assert rc != 0 and b"head_dim" in lib.gse_last_error()
+    rc = lib.gse_fill(None, 0, None, 0, None, 0, None, 0, None, None, -1, None, None, 0, None)
+    assert rc != 0
+    assert lib.gse_fill(None, 0, None, 0, None, 0, None, 0, None, None, 0, None, None, 0, None) == 0

@@ -1,0 +1,203 @@
+"""Decode path on the GPU through the C ABI: CSR fill, fused attention + scores, and the
+reference hook `after_decode`, against the CPU oracle."""
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from fakes import backend, layer
+
+pytestmark = pytest.mark.gpu
+
+ge = None
+
+
+@pytest.fixture(autouse=True)
+def fresh_state():
+    global ge
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    import gstar_evict
+    ge = gstar_evict
+    ge.STATE = None
+    yield
+    ge.STATE = None
+
+
+def test_fill_reads_compact_residents_then_tail():
+    """T:80-90 known answer."""
+    b = backend()
+    st = ge.state(b)
+    st.req_to_token[1, :10] = torch.arange(101, 111, dtype=torch.int32)
+    st.req_to_token[2, :6] = torch.arange(201, 207, dtype=torch.int32)
+    st.table[1, :4] = torch.tensor([101, 102, 106, 107], dtype=torch.int32)
+    st.count[1], st.frontier[1] = 4, 7
+    out = torch.full((32,), -1, dtype=torch.int64, device="cuda")
+    indptr = ge.fill(b, 2, torch.tensor([10, 6], device="cuda"), torch.tensor([1, 2], device="cuda"), out)
+    assert indptr.tolist() == [0, 7, 13]
+    assert out[:13].tolist() == [101, 102, 106, 107, 108, 109, 110, 201, 202, 203, 204, 205, 206]
+    out32 = torch.full((32,), -1, dtype=torch.int32, device="cuda")
+    ge.fill(b, 2, torch.tensor([10, 6], dtype=torch.int32, device="cuda"),
+            torch.tensor([1, 2], dtype=torch.int32, device="cuda"), out32)
+    assert out32[:13].tolist() == out[:13].tolist()
+
+
+def test_fill_matches_oracle_on_random_rows():
+    g = torch.Generator().manual_seed(11)
+    b = backend(rows=8, width=4096)
+    st = ge.state(b)
+    st.req_to_token.copy_(torch.randint(1, 20000, (8, 4096), generator=g, dtype=torch.int32))
+    st.table.copy_(torch.randint(1, 20000, (8, 4096), generator=g, dtype=torch.int32))
+    count = torch.randint(0, 1000, (8,), generator=g, dtype=torch.int32)
+    frontier = count + torch.randint(0, 500, (8,), generator=g, dtype=torch.int32)
+    st.count.copy_(count)
+    st.frontier.copy_(frontier)
+    rows = torch.tensor([5, 0, 7, 2, 3], device="cuda")
+    lens = frontier[rows.cpu()].long() + torch.randint(0, 2000, (5,), generator=g)
+    out = torch.full((40000,), -1, dtype=torch.int32, device="cuda")
+    indptr = ge.fill(b, 5, lens.cuda(), rows, out)
+    want_ptr, want = O.fill(st.table.cpu().numpy(), st.req_to_token.cpu().numpy(), rows.cpu().numpy(),
+                            lens.numpy(), frontier.numpy(), count.numpy())
+    assert indptr.tolist() == want_ptr.tolist()
+    assert out[:want.size].tolist() == want.tolist()
+
+
+def _decode_setup(lengths, seed=0, slots=20000):
+    g = torch.Generator().manual_seed(seed)
+    b = backend(gen=g, slots=slots)
+    st = ge.state(b)
+    heads, kv_heads, dim = 64, 8, 64
+    bs = len(lengths)
+    q = torch.randn((bs, heads, dim), generator=g).to(torch.bfloat16).cuda()
+    sinks = torch.randn(heads, generator=g).to(torch.bfloat16).cuda()
+    perm = (torch.randperm(slots - 1, generator=g)[:sum(lengths)] + 1).cuda()
+    indptr = torch.tensor(np.concatenate(([0], np.cumsum(lengths))), dtype=torch.int32, device="cuda")
+    rows = torch.arange(1, bs + 1, device="cuda")
+    return b, st, q, sinks, perm, indptr, rows
+
+
+def _oracle_step(b, st, q, sinks, perm, indptr, lid, mode):
+    keys = b.token_to_kv_pool.get_key_buffer(lid).float().cpu().numpy()
+    values = b.token_to_kv_pool.get_value_buffer(lid).float().cpu().numpy()
+    qn = q.float().cpu().numpy()
+    s = sinks.float().cpu().numpy()
+    ip = indptr.cpu().numpy()
+    pm = perm.cpu().numpy()
+    outs, norms = [], []
+    scores = np.zeros((st.kv_heads, keys.shape[0]))
+    for i in range(q.shape[0]):
+        slots = pm[ip[i]:ip[i + 1]]
+        o, norm = O.decode_attention(qn[i], keys, values, slots, s, 0.125)
+        outs.append(o)
+        norms.append(norm)
+        O.decode_scores_into(scores, qn[i], keys, slots, norm, 0.125, mode)
+    return np.stack(outs), np.stack(norms), scores
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("lag", [False, True])
+def test_fused_decode_matches_oracle(mode, lag):
+    lengths = [37, 1500, 3001]
+    b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths)
+    st.lag = lag
+    st.mode[:] = mode
+    b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=perm)
+    fb = SimpleNamespace(out_cache_loc=torch.zeros(3, dtype=torch.int64, device="cuda"), req_pool_indices=rows,
+                         seq_lens_cpu=torch.tensor(lengths))
+    o = torch.empty_like(q)
+    assert ge.decode(b, q.reshape(3, -1), layer(1), fb, sinks, o.reshape(3, -1))
+    if lag:
+        assert float(st.scores.abs().sum()) == 0.0  # the update is pending until flushed
+        # The flush rebuilds each row's list from the eviction state (empty table, tail = req_to_token).
+        for i, r in enumerate(rows.tolist()):
+            st.req_to_token[r, :lengths[i]] = perm[indptr[i]:indptr[i + 1]].int()
+        ge.flush(st)
+    want_o, want_norm, want_scores = _oracle_step(b, st, q, sinks, perm, indptr, 1, mode)
+    got_o = o.float().cpu().numpy()
+    # bf16 output: P is rounded to bf16 before the PV product, as in SGLang's decode kernel.
+    np.testing.assert_allclose(got_o, want_o, rtol=2e-2, atol=2e-2)
+    assert np.abs(got_o - want_o).mean() < 2e-3
+    expected = torch.zeros_like(st.scores)
+    expected[0] = torch.tensor(want_scores, dtype=torch.float32)
+    torch.testing.assert_close(st.scores, expected, rtol=2e-3, atol=1e-6)
+
+
+def test_lag_over_steps_equals_eager():
+    """Several decode steps with growing lists: lagged + flushed scores equal eager ones."""
+    g = torch.Generator().manual_seed(3)
+    results = {}
+    for lag in (False, True):
+        ge.STATE = None
+        b = backend(gen=torch.Generator().manual_seed(1))
+        st = ge.state(b)
+        st.lag = lag
+        st.mode[:] = 1
+        base = [100, 700]
+        perm = (torch.randperm(19999, generator=torch.Generator().manual_seed(2))[:2000] + 1).cuda()
+        qs = [torch.randn((2, 64, 64), generator=torch.Generator().manual_seed(10 + t)).to(torch.bfloat16).cuda()
+              for t in range(4)]
+        sinks = torch.randn(64, generator=torch.Generator().manual_seed(5)).cuda()
+        for t in range(4):
+            lens = [base[0] + t, base[1] + t]
+            idx = torch.cat((perm[:lens[0]], perm[1000:1000 + lens[1]]))
+            indptr = torch.tensor([0, lens[0], lens[0] + lens[1]], dtype=torch.int32, device="cuda")
+            b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=idx)
+            fb = SimpleNamespace(out_cache_loc=idx[indptr[1:].long() - 1], req_pool_indices=torch.tensor(
+                [1, 2], device="cuda"), seq_lens_cpu=torch.tensor(lens))
+            o = torch.empty((2, 64, 64), dtype=torch.bfloat16, device="cuda")
+            ge.decode(b, qs[t].reshape(2, -1), layer(1), fb, sinks, o.reshape(2, -1))
+        # Flushing needs the row view of the lists: table empty, tail = req_to_token.
+        st.req_to_token[1, :base[0] + 3] = perm[:base[0] + 3].int()
+        st.req_to_token[2, :base[1] + 3] = perm[1000:1000 + base[1] + 3].int()
+        ge.flush(st)
+        results[lag] = st.scores.clone()
+    torch.testing.assert_close(results[True], results[False], rtol=1e-6, atol=1e-9)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_after_decode_rebuilds_normaliser_from_split_lse(mode):
+    """T:48-78 with SGLang's split LSE layout (splits [1, 5, 8]) produced by the oracle."""
+    lengths = [37, 1500, 3001]
+    b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths, seed=4)
+    splits = [1, 5, 8]
+    keys = b.token_to_kv_pool.get_key_buffer(1).float().cpu().numpy()
+    lse = np.zeros((3, 64, 8), dtype=np.float32)
+    for i in range(3):
+        logits = O.decode_logits(q[i].float().cpu().numpy(), keys, perm[indptr[i]:indptr[i + 1]].cpu().numpy(), 0.125)
+        part, _ = O.split_lse(logits, splits[i])
+        lse[i, :, :splits[i]] = np.nan_to_num(part, nan=1e30)
+    b.forward_metadata = SimpleNamespace(attn_lse=torch.tensor(lse, device="cuda"), kv_indptr=indptr,
+                                         kv_indices=perm, num_kv_splits=torch.tensor(splits, dtype=torch.int32,
+                                                                                      device="cuda"))
+    st.mode[:] = mode
+    ge.after_decode(b, q.reshape(3, -1), layer(1), SimpleNamespace(
+        out_cache_loc=torch.zeros(3, dtype=torch.int64, device="cuda"), req_pool_indices=rows), sinks)
+    expected = torch.zeros_like(st.scores)
+    for i in range(3):
+        slots = perm[indptr[i]:indptr[i + 1]].long()
+        k = b.token_to_kv_pool.get_key_buffer(1)[slots].float().repeat_interleave(8, 1)
+        logits = torch.einsum("hd,khd->hk", q[i].float(), k) * 0.125
+        p = torch.softmax(torch.cat((logits, sinks.float()[:, None]), -1), -1)[:, :-1].view(8, 8, -1)
+        expected[0][:, slots] += p.sum(1) if mode == 1 else p.amax(1)
+    torch.testing.assert_close(st.scores, expected, rtol=2e-3, atol=1e-6)
+
+
+def test_rows_without_a_policy_get_no_scores_and_sliding_layers_are_skipped():
+    lengths = [64, 65]
+    b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths, seed=6)
+    st.mode[:] = 0
+    st.mode[2] = 2
+    st.lag = False
+    b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=perm)
+    fb = SimpleNamespace(out_cache_loc=torch.zeros(2, dtype=torch.int64, device="cuda"), req_pool_indices=rows,
+                         seq_lens_cpu=torch.tensor(lengths))
+    o = torch.empty_like(q)
+    assert not ge.decode(b, q.reshape(2, -1), SimpleNamespace(**{**vars(layer(0)), "sliding_window_size": 128}),
+                         fb, sinks, o.reshape(2, -1))
+    ge.decode(b, q.reshape(2, -1), layer(3), fb, sinks, o.reshape(2, -1))
+    touched = st.scores[1].abs().sum(0) > 0
+    assert not bool(touched[perm[:64]].any())
+    assert bool(touched[perm[64:]].all())
+    assert float(st.scores[0].abs().sum()) == 0.0
