@@ -1,0 +1,368 @@
+#!/usr/bin/env python
+"""Fused decode attention + H2O score + per-head eviction on one MI355X.
+
+Workload: the 12 full-attention layers of gpt-oss-20b (64 query heads, 8 KV
+heads, head_dim 64, bf16 K/V pool with 16-token pages), batch 32, logical
+lengths uniform in [16K, 64K] (seed 2), per-KV-head budget 32768 = 512 prefix
++ 4096 recent + 28160 scored (head_sum policy), eviction every 64 tokens per
+sequence, pre-compacted initial state, 2 % planted heavy-hitter keys. One step
+= the CSR fill, the fused attention + score kernel of every full layer, and
+every boundary (flush, select, relocate, compact) the step triggers.
+
+Prints one JSON line. ``value`` is the whole step's algorithmic HBM traffic
+divided by its time (GB/s); ``us_per_step`` is the step time.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from types import SimpleNamespace
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cache-eviction_amd"))
+sys.path.insert(0, ROOT)
+
+HQ, HKV, D = 64, 8, 64
+PAGE = 16
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=512)
+    p.add_argument("--warmup", type=int, default=16)
+    p.add_argument("--bs", type=int, default=32)
+    p.add_argument("--layers", type=int, default=12)
+    p.add_argument("--budget", type=int, default=32768)
+    p.add_argument("--prefix", type=int, default=512)
+    p.add_argument("--recent", type=int, default=4096)
+    p.add_argument("--interval", type=int, default=64)
+    p.add_argument("--min-len", type=int, default=16384)
+    p.add_argument("--max-len", type=int, default=65536)
+    p.add_argument("--policy", default="head_sum_2048")
+    p.add_argument("--heavy", type=float, default=0.02)
+    p.add_argument("--seed", type=int, default=2)
+    p.add_argument("--kernel-reps", type=int, default=20, help="launches timed per layer for the roofline")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--eager", action="store_true", help="score each step eagerly (second K read)")
+    return p.parse_args()
+
+
+def decode_bytes(n_resident):
+    """Algorithmic HBM bytes of one (sequence, full layer) decode step with n resident keys.
+
+    K and V rows (2 x 8 heads x 64 dims x 2 B), the fp32 score read + write per
+    KV head, the int32 slot index; then q in and o out (64 heads x 64 dims x
+    2 B each) and the 64 bf16 sinks read once per sequence.
+    """
+    return n_resident * (HKV * D * 2 * 2 + HKV * 4 * 2 + 4) + HQ * D * 2 * 2 + HQ * 2
+
+
+def boundary_bytes(n_cols, width, count, freed, layers):
+    """Algorithmic bytes of one row's boundary: select (score + pos read, kept pos write per head)
+    and compact (every kept middle K/V row and score read + written, table and leftover writes)."""
+    select = layers * HKV * (n_cols * (4 + 4) + count * 4)
+    move = layers * HKV * width * (2 * D * 2 * 2 + 4 * 2)
+    return select + move + 4 * count + 8 * freed
+
+
+class Workload:
+    """The synthetic serving state: pools, rows, eviction state, pre-drawn steps."""
+
+    def __init__(self, args, torch, ge):
+        self.args, self.torch, self.ge = args, torch, ge
+        dev = torch.device("cuda")
+        g = torch.Generator().manual_seed(args.seed)
+        self.dgen = torch.Generator(device=dev).manual_seed(args.seed)
+        bs, L, B = args.bs, args.layers, args.budget
+        total_steps = args.warmup + args.steps
+        lens = torch.randint(args.min_len, args.max_len + 1, (bs,), generator=g).tolist()
+        self.lens0 = lens
+        # Per-row state at the start: pre-compacted at the last interval boundary when over budget.
+        rows = []
+        for n in lens:
+            f = n - n % args.interval
+            if f > B:
+                rows.append({"len": n, "frontier": f, "count": B})
+            else:
+                rows.append({"len": n, "frontier": 0, "count": 0})
+        need = [r["count"] + (r["len"] - r["frontier"]) + total_steps + PAGE for r in rows]
+        pages = [-(-x // PAGE) for x in need]
+        npages = sum(pages)
+        perm = torch.randperm(npages, generator=g)  # page-granular interleaving of rows in the pool
+        slots = npages * PAGE + 1  # slot 0 stays the null slot
+        self.slots = slots
+        page_of = []
+        o = 0
+        for p in pages:
+            page_of.append(perm[o:o + p])
+            o += p
+        self.row_slots = [(pp[:, None] * PAGE + torch.arange(PAGE)[None, :]).reshape(-1) + 1 for pp in page_of]
+        width = max(lens) + total_steps + PAGE
+        width = -(-width // 256) * 256
+        # Pools: 12 full layers, random N(0, 1) bf16 with planted heavy hitters per KV head.
+        keys, values = {}, {}
+        for l in range(L):
+            k = torch.randn((slots, HKV, D), device=dev, dtype=torch.bfloat16)
+            v = torch.randn((slots, HKV, D), device=dev, dtype=torch.bfloat16)
+            gen = torch.Generator(device=dev).manual_seed(1000 + l)
+            u = torch.randn((HKV, D), device=dev, generator=gen)
+            u = u / u.norm(dim=-1, keepdim=True)
+            nh = int(args.heavy * slots)
+            for h in range(HKV):
+                idx = torch.randint(1, slots, (nh,), device=dev, generator=gen)
+                kk = k[idx, h].float()
+                k[idx, h] = (4 * kk.norm(dim=-1, keepdim=True) * u[h]).to(torch.bfloat16)
+            keys[l], values[l] = k, v
+        pool = SimpleNamespace(layers_mapping={l: (l, False) for l in range(L)},
+                               get_key_buffer=keys.__getitem__, get_value_buffer=values.__getitem__)
+        self.backend = SimpleNamespace(
+            token_to_kv_pool=pool, max_kv_splits=16,
+            req_to_token_pool=SimpleNamespace(req_to_token=torch.zeros((bs + 1, width), dtype=torch.int32,
+                                                                        device=dev)),
+            kv_indptr=torch.zeros(bs + 2, dtype=torch.int32, device=dev))
+        ge.STATE = None
+        st = ge.state(self.backend)
+        st.lag = not args.eager
+        self.st = st
+        st.scores.uniform_(0.0, 1.0, generator=torch.Generator(device=dev).manual_seed(7))
+        r2t = torch.zeros((bs + 1, width), dtype=torch.int32)
+        table = torch.zeros((bs + 1, width), dtype=torch.int32)
+        self.entries = []
+        self.new_slots = []
+        cfg = {"name": args.policy, "budget": B, "prefix": args.prefix, "recent": args.recent, "seed": args.seed}
+        for i, r in enumerate(rows):
+            row = i + 1
+            s = self.row_slots[i]
+            e = ge._live_entry(SimpleNamespace(rid=f"r{row}", session=None), cfg, "live")
+            n, f, c = r["len"], r["frontier"], r["count"]
+            if c:
+                # Columns: prefix, recent window (protected, by position), then a per-head sorted middle.
+                lo, hi = args.prefix, f - args.recent
+                mid = B - args.prefix - args.recent
+                pos = torch.empty((L, HKV, B), dtype=torch.int32)
+                pos[:, :, :args.prefix] = torch.arange(args.prefix, dtype=torch.int32)
+                pos[:, :, args.prefix:args.prefix + args.recent] = torch.arange(hi, f, dtype=torch.int32)
+                draw = torch.rand((L * HKV, hi - lo), device=dev, generator=self.dgen)
+                ranks = draw.argsort(-1)[:, :mid].sort(-1).values + lo
+                pos[:, :, args.prefix + args.recent:] = ranks.view(L, HKV, mid).to(torch.int32).cpu()
+                table[row, :c] = s[:c].int()
+                # req_to_token after the last repack: real slots from `true` on, packed owned slots first.
+                true = f - args.recent
+                r2t[row, true:f] = s[args.prefix:args.prefix + args.recent].int()
+                packed = torch.cat((s[:args.prefix], s[args.prefix + args.recent:c]))
+                r2t[row, :packed.numel()] = packed.int()
+                tail = s[c:c + n - f]
+                r2t[row, f:n] = tail.int()
+                e["pos"] = pos.to(dev)
+                e.update(frontier=f, count=c, last_boundary=f)
+                nxt = s[c + n - f:]
+            else:
+                r2t[row, :n] = s[:n].int()
+                nxt = s[n:]
+                e["last_boundary"] = n - n % args.interval
+            self.new_slots.append(nxt[:total_steps])
+            st.entries[row] = e
+            self.entries.append(e)
+            st.mode[row] = e["mode"]
+            st.count[row] = c
+            st.frontier[row] = f
+        st.req_to_token.copy_(r2t.to(dev))
+        st.table.copy_(table.to(dev))
+        self.new_slots = torch.stack(self.new_slots).to(dev)  # [bs, steps]
+        self.rows = torch.arange(1, bs + 1, device=dev)
+        self.lens = list(lens)
+        self.seq_lens = torch.tensor(lens, dtype=torch.int64, device=dev)
+        cap = sum(r["count"] + r["len"] - r["frontier"] for r in rows) + bs * (total_steps + 2)
+        self.kv_indices = torch.zeros(cap, dtype=torch.int32, device=dev)
+        self.q = [torch.randn((bs, HQ, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
+        self.sinks = [torch.randn(HQ, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+        self.o = [torch.empty((bs, HQ, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
+        self.layer_objs = [SimpleNamespace(sliding_window_size=-1, tp_q_head_num=HQ, tp_k_head_num=HKV,
+                                           qk_head_dim=D, layer_id=l, scaling=D ** -0.5) for l in range(L)]
+        self.alloc = SimpleNamespace(free_full=lambda s: None, full_to_swa_index_mapping=None)
+        self.step_index = 0
+        self.bytes = 0.0
+        self.boundaries = 0
+        self.resident_hist = []
+
+    def resident(self, i):
+        e = self.entries[i]
+        return e["count"] + self.lens[i] - e["frontier"]
+
+    def step(self, account=True):
+        torch, ge, st, a = self.torch, self.ge, self.st, self.args
+        # Boundaries before the new query (R:692-710): n tokens are cached.
+        for i, e in enumerate(self.entries):
+            n = self.lens[i]
+            if n % a.interval == 0 and n > e["last_boundary"]:
+                before = e["count"] + n - e["frontier"]
+                ge._boundary(st, i + 1, e, n, n - 256, self.alloc)
+                ev = e["events"][-1]
+                if account and "freed" in ev:
+                    width = ev["after"] - (a.prefix + a.recent)
+                    self.bytes += boundary_bytes(before, max(width, 0), ev["after"], ev["freed"], a.layers)
+                    self.boundaries += 1
+        # Allocate the new token's slot (SGLang's allocator), then the CSR for every full layer.
+        t = self.step_index
+        new = self.new_slots[:, t]
+        lens_t = self.seq_lens
+        st.req_to_token[self.rows, lens_t] = new.int()
+        self.seq_lens = lens_t + 1
+        self.lens = [n + 1 for n in self.lens]
+        bs = a.bs
+        ge.fill(self.backend, bs, self.seq_lens, self.rows, self.kv_indices)
+        self.backend.forward_metadata = SimpleNamespace(kv_indptr=self.backend.kv_indptr[:bs + 1],
+                                                        kv_indices=self.kv_indices)
+        fb = SimpleNamespace(out_cache_loc=new, req_pool_indices=self.rows, seq_lens_cpu=self.max_resident_list())
+        for l in range(a.layers):
+            ge.decode(self.backend, self.q[l].view(bs, -1), self.layer_objs[l], fb, self.sinks[l],
+                      self.o[l].view(bs, -1))
+        if account:
+            res = [self.resident(i) for i in range(bs)]
+            self.resident_hist.append(sum(res) / bs)
+            self.bytes += a.layers * sum(decode_bytes(r) for r in res)
+        self.step_index += 1
+
+    def max_resident_list(self):
+        # The split plan needs an upper bound of each row's resident count.
+        return [self.resident(i) for i in range(self.args.bs)]
+
+
+def kernel_roofline(w, reps):
+    """Average duration of the fused decode launch (split + merge kernels) over the last step's
+    inputs, with HIP events on the launch stream, and its algorithmic bytes per launch."""
+    torch, ge, a = w.torch, w.ge, w.args
+    bs = a.bs
+    fb = SimpleNamespace(out_cache_loc=w.new_slots[:, max(w.step_index - 1, 0)], req_pool_indices=w.rows,
+                         seq_lens_cpu=w.max_resident_list())
+    # Resident counts of the last step (the CSR already in kv_indices).
+    res = [w.resident(i) for i in range(bs)]
+    per_launch = sum(decode_bytes(r) for r in res)
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps * a.layers)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps * a.layers)]
+    k = 0
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        for l in range(a.layers):
+            starts[k].record(stream)
+            ge.decode(w.backend, w.q[l].view(bs, -1), w.layer_objs[l], fb, w.sinks[l], w.o[l].view(bs, -1))
+            ends[k].record(stream)
+            k += 1
+    torch.cuda.synchronize()
+    ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    avg_us = 1000 * statistics.mean(ms)
+    return per_launch, avg_us
+
+
+def cpu_baseline(w):
+    """Time the numpy oracle on a bounded sample of the same workload (2 sequences x 2 layers
+    decode at their real resident sets, one row-boundary's selection on 2 layers) and scale
+    to the full step (32 sequences x 12 layers, plus the measured boundary rate)."""
+    import numpy as np
+    import oracle as O
+    torch, a = w.torch, w.args
+    st = w.st
+    seqs, layers = 2, 2
+    t_dec = 0.0
+    for i in range(seqs):
+        row = i + 1
+        e = w.entries[i]
+        n = w.lens[i]
+        slots = torch.cat((st.table[row, :e["count"]], st.req_to_token[row, e["frontier"]:n])).long()
+        for l in range(layers):
+            keys = w.backend.token_to_kv_pool.get_key_buffer(l)[slots].float().cpu().numpy()
+            vals = w.backend.token_to_kv_pool.get_value_buffer(l)[slots].float().cpu().numpy()
+            q = w.q[l][i].float().cpu().numpy()
+            s = w.sinks[l].float().cpu().numpy()
+            local = np.arange(slots.numel())
+            t0 = time.perf_counter()
+            o, norm = O.decode_attention(q, keys, vals, local, s, D ** -0.5)
+            sc = np.zeros((HKV, slots.numel()))
+            O.decode_scores_into(sc, q, keys, local, norm, D ** -0.5, 1)
+            t_dec += time.perf_counter() - t0
+    per_seq_layer = t_dec / (seqs * layers)
+    # Boundary selection sample: the largest row's [2 layers, 8 heads, N] ranking.
+    i = max(range(a.bs), key=lambda j: w.resident(j))
+    e = w.entries[i]
+    N = w.resident(i)
+    pos = np.concatenate((e["pos"][:layers].cpu().numpy() if e["count"] else np.zeros((layers, HKV, 0), np.int32),
+                          np.broadcast_to(np.arange(e["frontier"], w.lens[i]), (layers, HKV, w.lens[i] - e["frontier"]))),
+                         -1)
+    score = np.random.default_rng(0).random(pos.shape)
+    t0 = time.perf_counter()
+    O.choose(a.policy, pos, w.lens[i] + (a.interval - w.lens[i] % a.interval), a.budget, a.prefix, a.recent, score)
+    t_sel = (time.perf_counter() - t0) * a.layers / layers
+    rate = w.boundaries / max(a.steps, 1)
+    us_step = 1e6 * (per_seq_layer * a.bs * a.layers + rate * t_sel)
+    return {"value": us_step, "unit": "us/step", "cores": 1, "kind": "port",
+            "sample": f"numpy float64 oracle: decode attention + head_sum scores for {seqs} sequences x {layers} "
+                      f"layers at their resident sets ({per_seq_layer * 1e3:.0f} ms each) scaled to {a.bs} x "
+                      f"{a.layers}; one {N}-column selection on {layers} layers scaled to {a.layers} layers at "
+                      f"{rate:.2f} boundaries/step"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    import gstar_evict as ge
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    w = Workload(args, torch, ge)
+    for _ in range(args.warmup):
+        w.step(account=False)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        w.step(account=True)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(end)
+    ms_step = gpu_ms / args.steps
+    gbs = w.bytes / (gpu_ms / 1000) / 1e9
+    per_launch, avg_us = kernel_roofline(w, args.kernel_reps)
+    achieved = per_launch / (avg_us * 1e-6) / 1e9
+    traffic = None
+    pmc = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    if os.path.exists(pmc):
+        traffic = json.load(open(pmc)).get("hbm_bytes_per_launch")
+    result = {
+        "metric": "fused attn+score+evict µs/decode-step & HBM GB/s (% peak), bs=32, 32K budget",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4), "us_per_step": round(1000 * ms_step, 1), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "gpt-oss-20b full-attention decode, 12 layers, bs=32, lengths U[16K,64K], "
+                               "budget 32768 (512+4096+28160), head_sum, evict every 64 steps, 16-token pages, "
+                               "2% heavy hitters",
+                   "batch": args.bs, "layers": args.layers, "budget": args.budget, "interval": args.interval,
+                   "policy": args.policy, "score_mode": "eager" if args.eager else "lag",
+                   "mean_resident": round(statistics.mean(w.resident_hist), 1),
+                   "boundaries": w.boundaries, "wall_s": round(wall, 3)},
+        "roofline": {"bound": "hbm", "kernel": "decode_split_kernel+decode_merge_kernel (one layer, bs=32)",
+                     "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": per_launch, "avg_launch_us": round(avg_us, 2)},
+        "step_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -98,7 +98,7 @@ struct ColSrc {
   // Scores for the boundary policies.
   int policy;
   const float* table_scores;
-  int64_t ssl, ssg;
+  int64_t ssl, ssg, sss;
   const int32_t* slots;
   const double* random_scores;
   int64_t seed;
@@ -183,7 +183,8 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
       } else if (a.src.policy == GSE_POLICY_RANDOM) {
         sc = a.src.random_scores[int64_t(lg) * N + c];
       } else {
-        sc = double(a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg + a.src.slots[c]]);
+        sc = double(a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg +
+                                       int64_t(a.src.slots[c]) * a.src.sss]);
       }
     }
     keys[c] = ordered_f64(sc);
@@ -334,7 +335,7 @@ struct BndArgs {
   void* const* v_pools;
   int64_t kv_ss, kv_sh;
   float* scores;
-  int64_t ssl, ssg;
+  int64_t ssl, ssg, sss;
   uint16_t* scratch_kv;
   float* scratch_sc;
 };
@@ -449,11 +450,11 @@ __global__ __launch_bounds__(256) void relocate_kernel(BndArgs a) {
   if (DIR == 0) {
     *reinterpret_cast<uint4*>(sk) = *reinterpret_cast<const uint4*>(K + src * a.kv_ss + off);
     *reinterpret_cast<uint4*>(sv) = *reinterpret_cast<const uint4*>(V + src * a.kv_ss + off);
-    if (piece == 0) a.scratch_sc[int64_t(lg) * a.budget + j] = srow[src];
+    if (piece == 0) a.scratch_sc[int64_t(lg) * a.budget + j] = srow[src * a.sss];
   } else {
     *reinterpret_cast<uint4*>(K + dst * a.kv_ss + off) = *reinterpret_cast<const uint4*>(sk);
     *reinterpret_cast<uint4*>(V + dst * a.kv_ss + off) = *reinterpret_cast<const uint4*>(sv);
-    if (piece == 0) srow[dst] = a.scratch_sc[int64_t(lg) * a.budget + j];
+    if (piece == 0) srow[dst * a.sss] = a.scratch_sc[int64_t(lg) * a.budget + j];
   }
 }
 
@@ -474,7 +475,7 @@ __global__ __launch_bounds__(256) void protected_pos_kernel(BndArgs a) {
 struct LiveArgs {
   float* scores;
   int layers, kv_heads;
-  int64_t ssl, ssg;
+  int64_t ssl, ssg, sss;
   const int32_t* table;
   int64_t table_stride;
   int32_t* r2t;
@@ -503,7 +504,7 @@ __global__ void zero_leftover_kernel(LiveArgs a) {
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
     const int64_t s = a.leftover[i % nl];
     const int64_t lg = i / nl;
-    a.scores[(lg / a.kv_heads) * a.ssl + (lg % a.kv_heads) * a.ssg + s] = 0.f;
+    a.scores[(lg / a.kv_heads) * a.ssl + (lg % a.kv_heads) * a.ssg + s * a.sss] = 0.f;
   }
 }
 
@@ -662,7 +663,7 @@ extern "C" int gse_select_kept(const int32_t* pos, const double* score, int laye
 
 extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s,
                             int64_t kv_stride_h, int kv_heads, int head_dim, float* scores, int64_t scores_stride_l,
-                            int64_t scores_stride_g, int32_t* table, int64_t table_stride,
+                            int64_t scores_stride_g, int64_t scores_stride_s, int32_t* table, int64_t table_stride,
                             const int32_t* req_to_token, int64_t r2t_stride, int32_t* frontier, int32_t* count, int row,
                             int64_t row_count, int64_t row_frontier, const int32_t* pos_old, int64_t pos_old_stride,
                             int64_t n, int64_t budget, int64_t prefix, int64_t recent, int64_t cursor, int has_cursor,
@@ -723,6 +724,7 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   b.scores = scores;
   b.ssl = scores_stride_l;
   b.ssg = scores_stride_g;
+  b.sss = scores_stride_s;
   b.scratch_kv = reinterpret_cast<uint16_t*>(ws + L.skv);
   b.scratch_sc = reinterpret_cast<float*>(ws + L.ssc);
 
@@ -738,6 +740,7 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   a.src.table_scores = scores;
   a.src.ssl = scores_stride_l;
   a.src.ssg = scores_stride_g;
+  a.src.sss = scores_stride_s;
   a.src.slots = b.slots;
   a.src.random_scores = random_scores;
   a.src.seed = seed;
@@ -777,7 +780,8 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
 }
 
 extern "C" int gse_boundary_live(float* scores, int layers, int64_t scores_stride_l, int kv_heads,
-                                 int64_t scores_stride_g, const int32_t* table, int64_t table_stride,
+                                 int64_t scores_stride_g, int64_t scores_stride_s, const int32_t* table,
+                                 int64_t table_stride,
                                  int32_t* req_to_token, int64_t r2t_stride, int row, int64_t n, int64_t true_len,
                                  const int64_t* leftover, const void* swa_mapping, int swa_dtype, int64_t num_slots,
                                  gse_boundary_status* status, void* workspace, int64_t workspace_bytes,
@@ -788,7 +792,7 @@ extern "C" int gse_boundary_live(float* scores, int layers, int64_t scores_strid
   if (workspace_bytes < gse_boundary_live_workspace_bytes(num_slots))
     return gse_fail(GSE_EWORKSPACE, "boundary_live: workspace too small");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  LiveArgs a = {scores, layers, kv_heads, scores_stride_l, scores_stride_g, table, table_stride, req_to_token,
+  LiveArgs a = {scores, layers, kv_heads, scores_stride_l, scores_stride_g, scores_stride_s, table, table_stride, req_to_token,
                 r2t_stride, row, n, true_len, leftover, swa_mapping, swa_dtype, num_slots, status,
                 static_cast<uint32_t*>(workspace)};
   // The kernels read the leftover count from *status; grid-stride loops cover any count.

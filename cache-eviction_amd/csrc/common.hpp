@@ -23,8 +23,12 @@ GSE_DEVICE uint16_t f32_to_bf16(float f) {
   return uint16_t(u >> 16);
 }
 
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+// Two floats to packed bf16 (round to nearest even): one v_cvt_pk_bf16_f32 on gfx950.
 GSE_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 GSE_DEVICE bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -36,6 +40,21 @@ GSE_DEVICE f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
 }
 
 GSE_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+
+// ds_read_b64_tr_b16: in each 16-lane group, source lane j supplies 4 consecutive
+// 16-bit values at its address; lane i receives value (i % 4) of source lanes
+// 4*e + i/4 for e = 0..3, i.e. one column of the 4 rows the group addressed.
+GSE_DEVICE s16x4_t ds_read_tr16(const uint16_t* lds) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)(lds));
+}
+
+GSE_DEVICE bf16x8_t join_bf16x8(s16x4_t lo, s16x4_t hi) {
+  typedef __attribute__((ext_vector_type(8))) short s16x8_t;
+  const s16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8_t, v);
+}
 
 template <typename T>
 GSE_DEVICE int64_t load_index(const void* p, int64_t i) {
@@ -52,6 +71,47 @@ GSE_DEVICE float load_float_dyn(const void* p, int dtype, int64_t i) {
 
 GSE_DEVICE float wave_max_xor(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, kWave)); }
 GSE_DEVICE float wave_sum_xor(float v, int mask) { return v + __shfl_xor(v, mask, kWave); }
+
+// Value of lane l ^ 16 (row swap), without LDS: v_permlane16_swap on gfx950.
+GSE_DEVICE float lane_xor16(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  // r[0] holds rows (0, 0, 2, 2) and r[1] rows (1, 1, 3, 3) of v: pick the other row of the pair.
+  const int row = (threadIdx.x >> 4) & 1;
+  return __uint_as_float(row ? r[0] : r[1]);
+}
+
+// Value of lane l ^ 32 (half swap), without LDS: v_permlane32_swap on gfx950.
+GSE_DEVICE float lane_xor32(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  // r[0] holds halves (0, 0) and r[1] halves (1, 1) of v.
+  const int half = (threadIdx.x >> 5) & 1;
+  return __uint_as_float(half ? r[0] : r[1]);
+}
+
+// max / sum of v over lanes l and l ^ 16 (resp. l ^ 32): the swap returns both halves of
+// each pair, so the symmetric reduction needs no lane-dependent select.
+GSE_DEVICE float xor16_max(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+GSE_DEVICE float xor16_sum(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+GSE_DEVICE float xor32_max(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+GSE_DEVICE float xor32_sum(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;

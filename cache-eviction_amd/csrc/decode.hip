@@ -12,15 +12,17 @@
 // merge. The score update of the pending query uses its final normaliser,
 // known since the previous call, so K is read once per step (GSE_SCORE_LAG).
 // GSE_SCORE_EAGER runs the attention pass, the merge, then a score-only pass.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace gse {
 
 constexpr int D = 64;        // head_dim
 constexpr int GROUP = 8;     // query heads per KV head
-constexpr int TILE = 32;     // keys per inner iteration (two 16-key MFMA sub-tiles)
+constexpr int TILE = 64;     // keys per inner iteration (four 16-key MFMA sub-tiles)
 constexpr int MAX_KVH = 8;   // waves per workgroup
-constexpr int LDS_ROW = D + 8;  // padded bf16 row of the V staging tile
+constexpr int LDS_ROW = D + 16;  // padded bf16 row of the V staging tile (160 B: transposed reads spread over banks)
 constexpr int PART = D + 4;     // floats per (sequence, split, head) partial: o[64], m, l, pad (16-byte rows)
 
 struct SlotSrc {
@@ -50,7 +52,7 @@ struct DecodeArgs {
   const void* rows;
   int rows_dtype;
   float* scores;
-  int64_t scores_sg;
+  int64_t scores_sg, scores_ss;
   // Score query / normaliser / length source.
   const uint16_t* sq;
   int64_t sq_sb, sq_sh;
@@ -78,6 +80,10 @@ GSE_DEVICE uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*
 
 // ATTN: attention partials for the current query. SCORE: score update of the
 // score query (pending or current). ROWVIEW: slot list from the eviction state.
+//
+// Software pipeline per 64-key tile t: the slot indices of tile t+2, then the
+// K/V rows and old scores of tile t+1 are issued before tile t is computed, so
+// no load on the critical path waits for a dependent load.
 template <bool ATTN, bool SCORE, bool ROWVIEW, typename IdxT>
 __global__ __launch_bounds__(512) void decode_split_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vtile[MAX_KVH][TILE * LDS_ROW];
@@ -156,159 +162,176 @@ __global__ __launch_bounds__(512) void decode_split_kernel(DecodeArgs a) {
   uint16_t* vt = vtile[g];
   float* srow = a.scores + int64_t(g) * a.scores_sg;
 
-  auto slot_at = [&](int64_t i) -> int64_t {
-    return i < k_end ? fetch_slot<ROWVIEW, IdxT>(a.src, row, base, cnt, fr, i) : int64_t(0);
+  // Slot of key i of this split (slot 0, the null slot, past the end).
+  auto slot_at = [&](int64_t i) -> int32_t {
+    return i < k_end ? int32_t(fetch_slot<ROWVIEW, IdxT>(a.src, row, base, cnt, fr, i)) : 0;
   };
-
   const int ntiles = int((k_end - k0 + TILE - 1) / TILE);
-  int64_t s0 = slot_at(k0 + col), s1 = slot_at(k0 + 16 + col);
-  uint4 ka0 = ld16(kbase + s0 * a.kv_ss), ka1 = ld16(kbase + s0 * a.kv_ss + 8);
-  uint4 kb0 = ld16(kbase + s1 * a.kv_ss), kb1 = ld16(kbase + s1 * a.kv_ss + 8);
-  uint4 va0 = {}, va1 = {}, vb0 = {}, vb1 = {};
-  if constexpr (ATTN) {
-    va0 = ld16(vbase + s0 * a.kv_ss);
-    va1 = ld16(vbase + s0 * a.kv_ss + 8);
-    vb0 = ld16(vbase + s1 * a.kv_ss);
-    vb1 = ld16(vbase + s1 * a.kv_ss + 8);
-  }
+  const bool score_live = SCORE && do_score;
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int64_t tb = k0 + int64_t(t) * TILE;
-    // Prefetch the next tile's rows.
-    const int64_t nb = tb + TILE;
-    int64_t n0 = 0, n1 = 0;
-    uint4 nka0 = {}, nka1 = {}, nkb0 = {}, nkb1 = {}, nva0 = {}, nva1 = {}, nvb0 = {}, nvb1 = {};
-    if (t + 1 < ntiles) {
-      n0 = slot_at(nb + col);
-      n1 = slot_at(nb + 16 + col);
-      nka0 = ld16(kbase + n0 * a.kv_ss);
-      nka1 = ld16(kbase + n0 * a.kv_ss + 8);
-      nkb0 = ld16(kbase + n1 * a.kv_ss);
-      nkb1 = ld16(kbase + n1 * a.kv_ss + 8);
+  // One 64-key tile: slots of keys (tb + 16*st + col), K/V 16-dim halves, old score of key tb + lane.
+  struct Tile {
+    int32_t s[4];
+    uint4 k[4][2], v[4][2];
+    float osc;
+  };
+  // Slot of the key this lane owns in the score update (sub-tile grp); no dynamic
+  // register indexing, so tiles stay in VGPRs.
+  auto own_slot = [&](const Tile& T) -> int32_t {
+    return grp == 0 ? T.s[0] : (grp == 1 ? T.s[1] : (grp == 2 ? T.s[2] : T.s[3]));
+  };
+  auto issue_rows = [&](Tile& T) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const uint16_t* kp = kbase + int64_t(T.s[st]) * a.kv_ss;
+      T.k[st][0] = ld16(kp);
+      T.k[st][1] = ld16(kp + 8);
       if constexpr (ATTN) {
-        nva0 = ld16(vbase + n0 * a.kv_ss);
-        nva1 = ld16(vbase + n0 * a.kv_ss + 8);
-        nvb0 = ld16(vbase + n1 * a.kv_ss);
-        nvb1 = ld16(vbase + n1 * a.kv_ss + 8);
+        const uint16_t* vp = vbase + int64_t(T.s[st]) * a.kv_ss;
+        T.v[st][0] = ld16(vp);
+        T.v[st][1] = ld16(vp + 8);
       }
     }
+    if (score_live) T.osc = srow[int64_t(own_slot(T)) * a.scores_ss];
+  };
 
+  // Compute tile t held in X. Lanes of group grp read the V^T fragments of keys
+  // 32*half + 16*h + 4*grp + e at dims 16*j + 4*(lane%4) (ds_read_b64_tr_b16).
+  auto compute = [&](int t, Tile& X) {
+    const int64_t tb = k0 + int64_t(t) * TILE;
     if constexpr (ATTN) {
       if (tb < attn_end) {
-        // Stage V rows [key][dim] for the transposed read.
-        *reinterpret_cast<uint4*>(vt + col * LDS_ROW + 16 * grp) = va0;
-        *reinterpret_cast<uint4*>(vt + col * LDS_ROW + 16 * grp + 8) = va1;
-        *reinterpret_cast<uint4*>(vt + (16 + col) * LDS_ROW + 16 * grp) = vb0;
-        *reinterpret_cast<uint4*>(vt + (16 + col) * LDS_ROW + 16 * grp + 8) = vb1;
-
-        f32x4_t sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
-        sa = mfma16x16x32(as_bf16x8(ka0), qc0, sa);
-        sa = mfma16x16x32(as_bf16x8(ka1), qc1, sa);
-        sb = mfma16x16x32(as_bf16x8(kb0), qc0, sb);
-        sb = mfma16x16x32(as_bf16x8(kb1), qc1, sb);
-        // sa[r]: head col, key tb + 4*grp + r; sb[r]: key tb + 16 + 4*grp + r.
-        float x[8];
-        float tmax = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t ka = tb + 4 * grp + r, kb = tb + 16 + 4 * grp + r;
-          x[r] = ka < attn_end ? sa[r] * a.scale2 : -INFINITY;
-          x[4 + r] = kb < attn_end ? sb[r] * a.scale2 : -INFINITY;
-          tmax = fmaxf(tmax, fmaxf(x[r], x[4 + r]));
+        for (int st = 0; st < 4; ++st) {
+          *reinterpret_cast<uint4*>(vt + (16 * st + col) * LDS_ROW + 16 * grp) = X.v[st][0];
+          *reinterpret_cast<uint4*>(vt + (16 * st + col) * LDS_ROW + 16 * grp + 8) = X.v[st][1];
         }
-        tmax = wave_max_xor(tmax, 16);
-        tmax = wave_max_xor(tmax, 32);
-        const float m_new = fmaxf(m_run, tmax);
-        const float corr = fast_exp2(m_run - m_new);
-        m_run = m_new;
+        // S^T sub-tiles: sc[st][r] = q.k (head col, key tb + 16*st + 4*grp + r), unscaled.
+        f32x4_t sc[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mfma16x16x32(as_bf16x8(X.k[st][0]), qc0, acc);
+          sc[st] = mfma16x16x32(as_bf16x8(X.k[st][1]), qc1, acc);
+        }
+        if (tb + TILE > attn_end) {  // only the last tile of a split is partial
+          const int lim = int(attn_end - tb);
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (16 * st + 4 * grp + r >= lim) sc[st][r] = -INFINITY;
+        }
+        float tmax = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                           fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+        tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(sc[2][0], sc[2][1]), fmaxf(sc[2][2], sc[2][3])),
+                                 fmaxf(fmaxf(sc[3][0], sc[3][1]), fmaxf(sc[3][2], sc[3][3]))));
+        tmax = xor32_max(xor16_max(tmax)) * a.scale2;  // log2 units (scale > 0)
+        // Lazy rescale: keep the running maximum unless some head's tile maximum
+        // exceeds it by more than 2^8 (exact: O and l share the reference).
+        if (__any(tmax > m_run + 8.f)) {
+          const float m_new = fmaxf(m_run, tmax);
+          const float corr = fast_exp2(m_run - m_new);
+          m_run = m_new;
+          l_run *= corr;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) oacc[j] = oacc[j] * corr;
+        }
         float psum = 0.f;
-        float p[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          p[e] = fast_exp2(x[e] - m_new);
-          psum += p[e];
-        }
-        l_run = l_run * corr + psum;
-        uint4 pk;
-        pk.x = pack_bf16x2(p[0], p[1]);
-        pk.y = pack_bf16x2(p[2], p[3]);
-        pk.z = pack_bf16x2(p[4], p[5]);
-        pk.w = pack_bf16x2(p[6], p[7]);
-        const bf16x8_t pb = as_bf16x8(pk);
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sc[st][r] = fast_exp2(fmaf(sc[st][r], a.scale2, -m_run));
+            psum += sc[st][r];
+          }
+        l_run += psum;
+        // P^T operands: half 0 covers sub-tiles 0/1, half 1 sub-tiles 2/3; k-element e maps to
+        // sub-tile 2*half + e/4, key 4*grp + e%4.
+        uint4 pa, pb;
+        pa.x = pack_bf16x2(sc[0][0], sc[0][1]);
+        pa.y = pack_bf16x2(sc[0][2], sc[0][3]);
+        pa.z = pack_bf16x2(sc[1][0], sc[1][1]);
+        pa.w = pack_bf16x2(sc[1][2], sc[1][3]);
+        pb.x = pack_bf16x2(sc[2][0], sc[2][1]);
+        pb.y = pack_bf16x2(sc[2][2], sc[2][3]);
+        pb.z = pack_bf16x2(sc[3][0], sc[3][1]);
+        pb.w = pack_bf16x2(sc[3][2], sc[3][3]);
         __builtin_amdgcn_wave_barrier();
-        // V^T fragment: dim (col + 16j), keys kappa(8*grp + e).
+        const uint16_t* vr = vt + (4 * grp + ((lane & 15) >> 2)) * LDS_ROW + 4 * (lane & 3);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint16_t* vc = vt + col + 16 * j;
-          uint4 av;
-          av.x = uint32_t(vc[(4 * grp + 0) * LDS_ROW]) | (uint32_t(vc[(4 * grp + 1) * LDS_ROW]) << 16);
-          av.y = uint32_t(vc[(4 * grp + 2) * LDS_ROW]) | (uint32_t(vc[(4 * grp + 3) * LDS_ROW]) << 16);
-          av.z = uint32_t(vc[(16 + 4 * grp + 0) * LDS_ROW]) | (uint32_t(vc[(16 + 4 * grp + 1) * LDS_ROW]) << 16);
-          av.w = uint32_t(vc[(16 + 4 * grp + 2) * LDS_ROW]) | (uint32_t(vc[(16 + 4 * grp + 3) * LDS_ROW]) << 16);
-          oacc[j] = oacc[j] * corr;
-          oacc[j] = mfma16x16x32(as_bf16x8(av), pb, oacc[j]);
+          const s16x4_t a0 = ds_read_tr16(vr + 16 * j);
+          const s16x4_t a1 = ds_read_tr16(vr + 16 * LDS_ROW + 16 * j);
+          const s16x4_t b0 = ds_read_tr16(vr + 32 * LDS_ROW + 16 * j);
+          const s16x4_t b1 = ds_read_tr16(vr + 48 * LDS_ROW + 16 * j);
+          oacc[j] = mfma16x16x32(join_bf16x8(a0, a1), as_bf16x8(pa), oacc[j]);
+          oacc[j] = mfma16x16x32(join_bf16x8(b0, b1), as_bf16x8(pb), oacc[j]);
         }
         __builtin_amdgcn_wave_barrier();
       }
     }
 
     if constexpr (SCORE) {
-      if (do_score && tb < score_end) {
-        f32x4_t pa = {0.f, 0.f, 0.f, 0.f}, pbv = {0.f, 0.f, 0.f, 0.f};
-        pa = mfma16x16x32(qp0, as_bf16x8(ka0), pa);
-        pa = mfma16x16x32(qp1, as_bf16x8(ka1), pa);
-        pbv = mfma16x16x32(qp0, as_bf16x8(kb0), pbv);
-        pbv = mfma16x16x32(qp1, as_bf16x8(kb1), pbv);
-        // pa[r]: head 4*grp + r, key tb + col; pbv[r]: key tb + 16 + col.
-        float ta, tbv;
-        if (grp < 2) {
-          float ua[4], ub[4];
+      if (score_live && tb < score_end) {
+        // Sp sub-tiles: logit_prev(head 4*grp + r, key tb + 16*st + col); heads 8..15 are padding.
+        float tot[4];
+        auto head_reduce = [&](auto is_max) {
+          constexpr bool MAX = decltype(is_max)::value;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            ua[r] = fast_exp2(pa[r] * a.scale2 - pn[r]);
-            ub[r] = fast_exp2(pbv[r] * a.scale2 - pn[r]);
+          for (int st = 0; st < 4; ++st) {
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+            acc = mfma16x16x32(qp0, as_bf16x8(X.k[st][0]), acc);
+            acc = mfma16x16x32(qp1, as_bf16x8(X.k[st][1]), acc);
+            const float u0 = fast_exp2(fmaf(acc[0], a.scale2, -pn[0]));
+            const float u1 = fast_exp2(fmaf(acc[1], a.scale2, -pn[1]));
+            const float u2 = fast_exp2(fmaf(acc[2], a.scale2, -pn[2]));
+            const float u3 = fast_exp2(fmaf(acc[3], a.scale2, -pn[3]));
+            // Combine head halves 0-3 (group 0) and 4-7 (group 1); groups 2, 3 carry padding.
+            tot[st] = MAX ? xor16_max(fmaxf(fmaxf(u0, u1), fmaxf(u2, u3))) : xor16_sum((u0 + u1) + (u2 + u3));
           }
-          if (max_mode) {
-            ta = fmaxf(fmaxf(ua[0], ua[1]), fmaxf(ua[2], ua[3]));
-            tbv = fmaxf(fmaxf(ub[0], ub[1]), fmaxf(ub[2], ub[3]));
-          } else {
-            ta = (ua[0] + ua[1]) + (ua[2] + ua[3]);
-            tbv = (ub[0] + ub[1]) + (ub[2] + ub[3]);
-          }
-        } else {
-          ta = 0.f;
-          tbv = 0.f;
-        }
-        const float oa = __shfl_xor(ta, 16, kWave), ob = __shfl_xor(tbv, 16, kWave);
-        if (max_mode) {
-          ta = fmaxf(ta, oa);
-          tbv = fmaxf(tbv, ob);
-        } else {
-          ta += oa;
-          tbv += ob;
-        }
-        // Lane l < 32 owns key tb + l: sub-tile 0 for l < 16, sub-tile 1 for 16 <= l < 32.
-        if (lane < 32) {
-          const int64_t key = tb + lane;
-          if (key < score_end) {
-            const int64_t slot = lane < 16 ? s0 : s1;
-            const float val = lane < 16 ? ta : tbv;
-            srow[slot] = srow[slot] + val;
-          }
-        }
+        };
+        if (max_mode)
+          head_reduce(std::true_type{});
+        else
+          head_reduce(std::false_type{});
+        // Lanes < 32 hold every sub-tile's totals; lane l owns key tb + l (sub-tile l/16, column l%16).
+        const float send = grp == 0 ? tot[2] : tot[3];
+        const float recv = lane_xor32(send);
+        const float val = grp == 0 ? tot[0] : (grp == 1 ? tot[1] : recv);
+        if (tb + lane < score_end) srow[int64_t(own_slot(X)) * a.scores_ss] = X.osc + val;
       }
     }
+  };
 
-    s0 = n0;
-    s1 = n1;
-    ka0 = nka0; ka1 = nka1; kb0 = nkb0; kb1 = nkb1;
-    va0 = nva0; va1 = nva1; vb0 = nvb0; vb1 = nvb1;
+  // Pipeline: slots two tiles ahead, rows and old scores one tile ahead. The K/V
+  // buffers alternate between A and B, so no register copies are needed.
+  Tile A, B;
+  int32_t s_ahead[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    A.s[st] = slot_at(k0 + 16 * st + col);
+    B.s[st] = ntiles > 1 ? slot_at(k0 + TILE + 16 * st + col) : 0;
+  }
+  A.osc = B.osc = 0.f;
+  issue_rows(A);
+  auto step = [&](int t, Tile& X, Tile& Y) {
+    const int64_t tb = k0 + int64_t(t) * TILE;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) s_ahead[st] = t + 2 < ntiles ? slot_at(tb + 2 * TILE + 16 * st + col) : 0;
+    if (t + 1 < ntiles) issue_rows(Y);
+    compute(t, X);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) X.s[st] = s_ahead[st];
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, A, B);
+    if (t + 1 < ntiles) step(t + 1, B, A);
   }
 
   if constexpr (ATTN) {
     if (k0 < attn_end) {
-      float lt = wave_sum_xor(l_run, 16);
-      lt = wave_sum_xor(lt, 32);
+      const float lt = xor32_sum(xor16_sum(l_run));
       if (col < GROUP) {
         float* pp = a.part + ((int64_t(b) * a.max_splits + split) * a.q_heads + hq) * PART;
 #pragma unroll
@@ -342,11 +365,11 @@ struct MergeArgs {
   int q_heads, chunk, max_splits;
 };
 
-// One workgroup per sequence; thread t handles head t/4, dims [16*(t%4), +16).
+// Grid (bs, q_heads / 4): a workgroup merges 4 heads; thread (head t/64, dim t%64).
 __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   const int b = blockIdx.x;
-  const int h = threadIdx.x >> 2;
-  const int dq = threadIdx.x & 3;
+  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int d = threadIdx.x & 63;
   if (h >= a.q_heads) return;
   const int64_t len = int64_t(a.indptr[b + 1]) - a.indptr[b];
   int nsplit = int((len + a.chunk - 1) / a.chunk);
@@ -357,51 +380,28 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   float mx = sink2;
   for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, pb[s * sstride + D]);
   float lsum = fast_exp2(sink2 - mx);
-  float acc[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  float acc = 0.f;
   for (int s = 0; s < nsplit; ++s) {
     const float* ps = pb + s * sstride;
     const float w = fast_exp2(ps[D] - mx);
     lsum += w * ps[D + 1];
-#pragma unroll
-    for (int i = 0; i < 16; i += 4) {
-      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(ps + 16 * dq + i);
-      acc[i] += w * v[0];
-      acc[i + 1] += w * v[1];
-      acc[i + 2] += w * v[2];
-      acc[i + 3] += w * v[3];
-    }
+    acc += w * ps[d];
   }
-  const float inv = 1.f / lsum;
-  uint4 w0, w1;
-  w0.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
-  w0.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
-  w0.z = pack_bf16x2(acc[4] * inv, acc[5] * inv);
-  w0.w = pack_bf16x2(acc[6] * inv, acc[7] * inv);
-  w1.x = pack_bf16x2(acc[8] * inv, acc[9] * inv);
-  w1.y = pack_bf16x2(acc[10] * inv, acc[11] * inv);
-  w1.z = pack_bf16x2(acc[12] * inv, acc[13] * inv);
-  w1.w = pack_bf16x2(acc[14] * inv, acc[15] * inv);
-  uint16_t* op = a.o + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + 16 * dq;
-  *reinterpret_cast<uint4*>(op) = w0;
-  *reinterpret_cast<uint4*>(op + 8) = w1;
+  a.o[int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + d] = f32_to_bf16(acc / lsum);
   const float norm = (mx + __log2f(lsum)) * kLn2;
-  if (a.norm_out && dq == 0) a.norm_out[int64_t(b) * a.q_heads + h] = norm;
+  if (a.norm_out && d == 0) a.norm_out[int64_t(b) * a.q_heads + h] = norm;
   if (a.pq) {
     const int64_t row = load_index_dyn(a.rows, a.rows_dtype, b);
     const int md = a.mode[row];
     const bool live = md == 1 || md == 2;
     if (live) {
-      const uint16_t* qs = a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + 16 * dq;
-      uint16_t* qd = a.pq + (row * a.q_heads + h) * D + 16 * dq;
-      *reinterpret_cast<uint4*>(qd) = ld16(qs);
-      *reinterpret_cast<uint4*>(qd + 8) = ld16(qs + 8);
-      if (dq == 0) a.pnorm[row * a.q_heads + h] = norm;
+      a.pq[(row * a.q_heads + h) * D + d] = a.q[int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + d];
+      if (d == 0) a.pnorm[row * a.q_heads + h] = norm;
     }
-    if (threadIdx.x == 0) a.plen[row] = live ? int32_t(len) : 0;
+    if (blockIdx.y == 0 && threadIdx.x == 0) a.plen[row] = live ? int32_t(len) : 0;
   }
 }
+
 
 struct NormArgs {
   const float* lse;
@@ -459,7 +459,7 @@ int check_decode_shape(int q_heads, int kv_heads, int head_dim, int chunk, int m
   if (head_dim != D) return gse_fail(GSE_ESHAPE, "decode: head_dim must be 64");
   if (kv_heads < 1 || kv_heads > MAX_KVH || q_heads != GROUP * kv_heads)
     return gse_fail(GSE_ESHAPE, "decode: need q_heads == 8 * kv_heads and 1 <= kv_heads <= 8");
-  if (chunk < TILE || chunk % TILE) return gse_fail(GSE_EINVAL, "decode: chunk must be a positive multiple of 32");
+  if (chunk < TILE || chunk % TILE) return gse_fail(GSE_EINVAL, "decode: chunk must be a positive multiple of 64");
   if (max_splits < 1 || max_splits > 65535) return gse_fail(GSE_EINVAL, "decode: max_splits out of range");
   return GSE_OK;
 }
@@ -481,7 +481,7 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
                           const int32_t* kv_indptr, const void* kv_indices, int indices_dtype,
                           const void* sinks, int sinks_dtype, const int32_t* mode_by_row, const void* rows,
-                          int rows_dtype, float* scores, int64_t scores_stride_g,
+                          int rows_dtype, float* scores, int64_t scores_stride_g, int64_t scores_stride_s,
                           void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
                           void* pend_q, float* pend_norm, int32_t* pend_len,
                           int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int chunk,
@@ -525,6 +525,7 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   a.rows_dtype = rows_dtype;
   a.scores = scores;
   a.scores_sg = scores_stride_g;
+  a.scores_ss = scores_stride_s;
   a.part = part;
   a.q_heads = q_heads;
   a.kv_heads = kv_heads;
@@ -567,7 +568,7 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   } else {
     if ((rc = launch_split<true, false, false>(a, indices_dtype, bs, s))) return rc;
   }
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(bs), dim3(256), 0, s, m);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(bs, (q_heads + 3) / 4), dim3(256), 0, s, m);
   if ((rc = gse_launch_check("decode_merge"))) return rc;
   if (score_mode == GSE_SCORE_EAGER) {
     a.sq = a.q;
@@ -586,7 +587,8 @@ extern "C" int gse_decode_flush(const void* k_pool, int64_t kv_stride_s, int64_t
                                 const int32_t* table, int64_t table_stride, const int32_t* req_to_token,
                                 int64_t r2t_stride, int64_t r2t_width, const int32_t* frontier, const int32_t* count,
                                 const int32_t* mode_by_row, const void* rows, int rows_dtype, int n_rows,
-                                float* scores, int64_t scores_stride_g, void* pend_q, float* pend_norm,
+                                float* scores, int64_t scores_stride_g, int64_t scores_stride_s, void* pend_q,
+                                float* pend_norm,
                                 int32_t* pend_len, int q_heads, int kv_heads, int head_dim, float sm_scale,
                                 int chunk, int max_splits, gse_stream_t stream) {
   if (int rc = check_decode_shape(q_heads, kv_heads, head_dim, chunk, max_splits)) return rc;
@@ -612,6 +614,7 @@ extern "C" int gse_decode_flush(const void* k_pool, int64_t kv_stride_s, int64_t
   a.rows_dtype = rows_dtype;
   a.scores = scores;
   a.scores_sg = scores_stride_g;
+  a.scores_ss = scores_stride_s;
   a.sq = static_cast<const uint16_t*>(pend_q);
   a.sq_sb = int64_t(q_heads) * D;
   a.sq_sh = D;
@@ -638,7 +641,8 @@ extern "C" int gse_decode_scores_from_lse(const void* q, int64_t q_stride_b, int
                                           const int32_t* num_kv_splits, int max_kv_splits, int min_block_kv,
                                           const void* sinks, int sinks_dtype, const int32_t* mode_by_row,
                                           const void* rows, int rows_dtype, float* scores,
-                                          int64_t scores_stride_g, int bs, int q_heads, int kv_heads,
+                                          int64_t scores_stride_g, int64_t scores_stride_s, int bs, int q_heads,
+                                          int kv_heads,
                                           int head_dim, float sm_scale, int chunk, int max_splits, void* workspace,
                                           int64_t workspace_bytes, gse_stream_t stream) {
   if (int rc = check_decode_shape(q_heads, kv_heads, head_dim, chunk, max_splits)) return rc;
@@ -666,6 +670,7 @@ extern "C" int gse_decode_scores_from_lse(const void* q, int64_t q_stride_b, int
   a.rows_dtype = rows_dtype;
   a.scores = scores;
   a.scores_sg = scores_stride_g;
+  a.scores_ss = scores_stride_s;
   a.sq = static_cast<const uint16_t*>(q);
   a.sq_sb = q_stride_b;
   a.sq_sh = q_stride_h;

@@ -57,13 +57,13 @@ __global__ __launch_bounds__(256) void fill_kernel(FillArgs a) {
 
 template <typename SlotT>
 __global__ void zero_slots_kernel(float* scores, int layers, int64_t layer_stride, int kv_heads, int64_t head_stride,
-                                  const SlotT* slots, int64_t n) {
+                                  int64_t slot_stride, const SlotT* slots, int64_t n) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n * layers * kv_heads) return;
   const int64_t s = i % n;
   const int64_t lg = i / n;
   const int64_t g = lg % kv_heads, l = lg / kv_heads;
-  scores[l * layer_stride + g * head_stride + int64_t(slots[s])] = 0.f;
+  scores[l * layer_stride + g * head_stride + int64_t(slots[s]) * slot_stride] = 0.f;
 }
 
 }  // namespace gse
@@ -89,7 +89,7 @@ extern "C" int gse_fill(const int32_t* table, int64_t table_stride, const int32_
 }
 
 extern "C" int gse_zero_slots(float* scores, int layers, int64_t layer_stride, int kv_heads, int64_t head_stride,
-                              const void* slots, int slots_dtype, int64_t n, gse_stream_t stream) {
+                              int64_t slot_stride, const void* slots, int slots_dtype, int64_t n, gse_stream_t stream) {
   if (n < 0 || layers < 0 || kv_heads < 0) return gse_fail(GSE_EINVAL, "zero_slots: negative size");
   const int64_t total = n * layers * kv_heads;
   if (total == 0) return GSE_OK;
@@ -98,9 +98,9 @@ extern "C" int gse_zero_slots(float* scores, int layers, int64_t layer_stride, i
   const dim3 grid(unsigned((total + 255) / 256));
   if (slots_dtype == GSE_I64)
     hipLaunchKernelGGL(zero_slots_kernel<int64_t>, grid, dim3(256), 0, s, scores, layers, layer_stride, kv_heads,
-                       head_stride, static_cast<const int64_t*>(slots), n);
+                       head_stride, slot_stride, static_cast<const int64_t*>(slots), n);
   else
     hipLaunchKernelGGL(zero_slots_kernel<int32_t>, grid, dim3(256), 0, s, scores, layers, layer_stride, kv_heads,
-                       head_stride, static_cast<const int32_t*>(slots), n);
+                       head_stride, slot_stride, static_cast<const int32_t*>(slots), n);
   return gse_launch_check("zero_slots");
 }

@@ -29,23 +29,23 @@ SIGNATURES = {
     "gse_version": (_i, []),
     "gse_last_error": (ctypes.c_char_p, []),
     "gse_fill": (_i, [_p, _l, _p, _l, _p, _i, _p, _i, _p, _p, _i, _p, _p, _i, _p]),
-    "gse_zero_slots": (_i, [_p, _i, _l, _i, _l, _p, _i, _l, _p]),
+    "gse_zero_slots": (_i, [_p, _i, _l, _i, _l, _l, _p, _i, _l, _p]),
     "gse_decode_workspace_bytes": (_l, [_i, _i, _i, _i]),
-    "gse_decode": (_i, [_p, _l, _l, _p, _p, _l, _l, _p, _p, _i, _p, _i, _p, _p, _i, _p, _l, _p, _l, _l, _p,
+    "gse_decode": (_i, [_p, _l, _l, _p, _p, _l, _l, _p, _p, _i, _p, _i, _p, _p, _i, _p, _l, _l, _p, _l, _l, _p,
                         _p, _p, _p, _i, _i, _i, _i, _f, _i, _i, _i, _p, _l, _p]),
-    "gse_decode_flush": (_i, [_p, _l, _l, _p, _l, _p, _l, _l, _p, _p, _p, _p, _i, _i, _p, _l, _p, _p, _p,
+    "gse_decode_flush": (_i, [_p, _l, _l, _p, _l, _p, _l, _l, _p, _p, _p, _p, _i, _i, _p, _l, _l, _p, _p, _p,
                               _i, _i, _i, _f, _i, _i, _p]),
     "gse_decode_scores_from_lse": (_i, [_p, _l, _l, _p, _l, _l, _p, _p, _i, _p, _l, _l, _p, _i, _i, _p, _i,
-                                        _p, _p, _i, _p, _l, _i, _i, _i, _i, _f, _i, _i, _p, _l, _p]),
+                                        _p, _p, _i, _p, _l, _l, _i, _i, _i, _i, _f, _i, _i, _p, _l, _p]),
     "gse_reservoir_scores": (_i, [_p, _i, _p, _p, _i, _i, _l, _l, _p, _p]),
     "gse_select_kept": (_i, [_p, _p, _i, _i, _l, _l, _l, _l, _l, _l, _i, _i, _p, _p, _p, _l, _p]),
     "gse_boundary_workspace_bytes": (_l, [_i, _i, _i, _l, _l, _l]),
-    "gse_boundary": (_i, [_p, _p, _i, _l, _l, _i, _i, _p, _l, _l, _p, _l, _p, _l, _p, _p, _i, _l, _l, _p, _l,
+    "gse_boundary": (_i, [_p, _p, _i, _l, _l, _i, _i, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _i, _l, _l, _p, _l,
                           _l, _l, _l, _l, _l, _i, _i, _l, _p, _p, _p, _p, _p, _l, _p]),
     "gse_boundary_live_workspace_bytes": (_l, [_l]),
-    "gse_boundary_live": (_i, [_p, _i, _l, _i, _l, _p, _l, _p, _l, _i, _l, _l, _p, _p, _i, _l, _p, _p, _l, _p]),
+    "gse_boundary_live": (_i, [_p, _i, _l, _i, _l, _l, _p, _l, _p, _l, _i, _l, _l, _p, _p, _i, _l, _p, _p, _l, _p]),
     "gse_prefill_workspace_bytes": (_l, [_l, _i]),
-    "gse_prefill_scores": (_i, [_p, _l, _l, _l, _p, _l, _l, _p, _i, _l, _l, _p, _i, _i, _p, _l, _i, _i, _i,
+    "gse_prefill_scores": (_i, [_p, _l, _l, _l, _p, _l, _l, _p, _i, _l, _l, _p, _i, _i, _p, _l, _l, _i, _i, _i,
                                 _f, _p, _l, _p]),
 }
 

@@ -14,7 +14,9 @@
  *
  * Layouts (the reference's, R:89-110):
  *   K/V pool of one layer   bf16 [slots, kv_heads, head_dim], head_dim contiguous
- *   scores                  fp32 [full layers, kv_heads, slots] (any strides)
+ *   scores                  fp32 [full layers, kv_heads, slots] with explicit strides; the
+ *                           runtime keeps the KV heads of a slot adjacent (strides
+ *                           slots*kv_heads, 1, kv_heads), so one page's scores fill whole lines
  *   table / req_to_token    int32 [rows, width]
  *   frontier / count / mode int32 [rows]
  *   pos (per row)           int32 [full layers, kv_heads, count]
@@ -92,7 +94,7 @@ int gse_fill(const int32_t* table, int64_t table_stride, const int32_t* req_to_t
  * Replaces R:211-212 / R:293-294 (`st.scores.index_fill_(2, out_cache_loc, 0.0)`).
  */
 int gse_zero_slots(float* scores, int layers, int64_t layer_stride, int kv_heads, int64_t head_stride,
-                   const void* slots, int slots_dtype, int64_t n, gse_stream_t stream);
+                   int64_t slot_stride, const void* slots, int slots_dtype, int64_t n, gse_stream_t stream);
 
 /* Workspace bytes gse_decode / gse_decode_scores_from_lse need for bs sequences and max_splits splits. */
 int64_t gse_decode_workspace_bytes(int bs, int max_splits, int q_heads, int head_dim);
@@ -118,7 +120,7 @@ int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
                const int32_t* kv_indptr, const void* kv_indices, int indices_dtype,
                const void* sinks, int sinks_dtype, const int32_t* mode_by_row, const void* rows, int rows_dtype,
-               float* scores, int64_t scores_stride_g,
+               float* scores, int64_t scores_stride_g, int64_t scores_stride_s,
                void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
                void* pend_q, float* pend_norm, int32_t* pend_len,
                int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int chunk, int max_splits,
@@ -135,7 +137,7 @@ int gse_decode_flush(const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_
                      const int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
                      int64_t r2t_width, const int32_t* frontier, const int32_t* count, const int32_t* mode_by_row,
                      const void* rows, int rows_dtype, int n_rows,
-                     float* scores, int64_t scores_stride_g,
+                     float* scores, int64_t scores_stride_g, int64_t scores_stride_s,
                      void* pend_q, float* pend_norm, int32_t* pend_len,
                      int q_heads, int kv_heads, int head_dim, float sm_scale, int chunk, int max_splits,
                      gse_stream_t stream);
@@ -155,6 +157,7 @@ int gse_decode_scores_from_lse(const void* q, int64_t q_stride_b, int64_t q_stri
                                const int32_t* num_kv_splits, int max_kv_splits, int min_block_kv,
                                const void* sinks, int sinks_dtype, const int32_t* mode_by_row,
                                const void* rows, int rows_dtype, float* scores, int64_t scores_stride_g,
+                               int64_t scores_stride_s,
                                int bs, int q_heads, int kv_heads, int head_dim, float sm_scale,
                                int chunk, int max_splits, void* workspace, int64_t workspace_bytes,
                                gse_stream_t stream);
@@ -201,6 +204,7 @@ int64_t gse_boundary_workspace_bytes(int layers, int kv_heads, int head_dim, int
  */
 int gse_boundary(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
                  int kv_heads, int head_dim, float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                 int64_t scores_stride_s,
                  int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
                  int32_t* frontier, int32_t* count, int row, int64_t row_count, int64_t row_frontier,
                  const int32_t* pos_old, int64_t pos_old_stride, int64_t n, int64_t budget, int64_t prefix,
@@ -224,6 +228,7 @@ int64_t gse_boundary_live_workspace_bytes(int64_t num_slots);
  * leftover slots (status.leftover of them) once the stream completes.
  */
 int gse_boundary_live(float* scores, int layers, int64_t scores_stride_l, int kv_heads, int64_t scores_stride_g,
+                      int64_t scores_stride_s,
                       const int32_t* table, int64_t table_stride, int32_t* req_to_token, int64_t r2t_stride,
                       int row, int64_t n, int64_t true_len, const int64_t* leftover, const void* swa_mapping,
                       int swa_dtype, int64_t num_slots, gse_boundary_status* status, void* workspace,
@@ -244,6 +249,7 @@ int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_stride_h, in
                        const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_h,
                        const void* slots, int slots_dtype, int64_t total, int64_t prefix_len,
                        const void* sinks, int sinks_dtype, int mode, float* scores, int64_t scores_stride_g,
+                       int64_t scores_stride_s,
                        int q_heads, int kv_heads, int head_dim, float sm_scale,
                        void* workspace, int64_t workspace_bytes, gse_stream_t stream);
 

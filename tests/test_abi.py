@@ -57,7 +57,7 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     if not os.path.exists(_native.LIB_PATH):
         pytest.skip("library not built")
     lib = _native.lib()
-    rc = lib.gse_decode(None, 0, 0, None, None, 0, 0, None, None, 0, None, 0, None, None, 0, None, 0, None, 0, 0,
+    rc = lib.gse_decode(None, 0, 0, None, None, 0, 0, None, None, 0, None, 0, None, None, 0, None, 0, 1, None, 0, 0,
                         None, None, None, None, 4, 64, 8, 128, 0.125, 512, 8, 0, None, 0, None)
     assert rc != 0 and b"head_dim" in lib.gse_last_error()
     rc = lib.gse_fill(None, 0, None, 0, None, 0, None, 0, None, None, -1, None, None, 0, None)
