@@ -51,6 +51,9 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=20, help="launches timed per layer for the roofline")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--eager", action="store_true", help="score each step eagerly (second K read)")
+    p.add_argument("--copy-mib", type=int, default=0,
+                   help="only run a plain device copy of this many MiB (5 launches): the byte-counter "
+                        "calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE runs")
     return p.parse_args()
 
 
@@ -309,6 +312,24 @@ def cpu_baseline(w):
                       f"{rate:.2f} boundaries/step"}
 
 
+def copy_calibration(torch, mib):
+    """A plain device-to-device copy of `mib` MiB, five times, timed with events."""
+    n = mib * (1 << 20)
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(5):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / 5
+    print(json.dumps({"copy_bytes": n, "read_plus_write_GBs": round(2 * n / (ms * 1e-3) / 1e9, 1),
+                      "avg_ms": round(ms, 4)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -320,6 +341,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if args.copy_mib:
+        copy_calibration(torch, args.copy_mib)
+        return
     w = Workload(args, torch, ge)
     for _ in range(args.warmup):
         w.step(account=False)

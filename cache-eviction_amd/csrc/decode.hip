@@ -162,9 +162,12 @@ __global__ __launch_bounds__(512) void decode_split_kernel(DecodeArgs a) {
   uint16_t* vt = vtile[g];
   float* srow = a.scores + int64_t(g) * a.scores_sg;
 
-  // Slot of key i of this split (slot 0, the null slot, past the end).
+  // Slot of key i of this split (slot 0, the null slot, past the end). The index load is
+  // issued unconditionally (clamped to the last key) so every path issues the same loads and
+  // the compiler's wait counts stay exact.
   auto slot_at = [&](int64_t i) -> int32_t {
-    return i < k_end ? int32_t(fetch_slot<ROWVIEW, IdxT>(a.src, row, base, cnt, fr, i)) : 0;
+    const int32_t s = int32_t(fetch_slot<ROWVIEW, IdxT>(a.src, row, base, cnt, fr, i < k_end ? i : k_end - 1));
+    return i < k_end ? s : 0;
   };
   const int ntiles = int((k_end - k0 + TILE - 1) / TILE);
   const bool score_live = SCORE && do_score;
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(512) void decode_split_kernel(DecodeArgs a) {
         T.v[st][1] = ld16(vp + 8);
       }
     }
-    if (score_live) T.osc = srow[int64_t(own_slot(T)) * a.scores_ss];
+    if constexpr (SCORE) T.osc = srow[int64_t(score_live ? own_slot(T) : 0) * a.scores_ss];
   };
 
   // Compute tile t held in X. Lanes of group grp read the V^T fragments of keys
@@ -311,15 +314,20 @@ __global__ __launch_bounds__(512) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
     A.s[st] = slot_at(k0 + 16 * st + col);
-    B.s[st] = ntiles > 1 ? slot_at(k0 + TILE + 16 * st + col) : 0;
+    B.s[st] = slot_at(k0 + TILE + 16 * st + col);
   }
   A.osc = B.osc = 0.f;
   issue_rows(A);
   auto step = [&](int t, Tile& X, Tile& Y) {
     const int64_t tb = k0 + int64_t(t) * TILE;
+    // Past the last tile the slots are 0: the null slot's rows are loaded (one cached line per
+    // wave) instead of branching around the loads.
 #pragma unroll
-    for (int st = 0; st < 4; ++st) s_ahead[st] = t + 2 < ntiles ? slot_at(tb + 2 * TILE + 16 * st + col) : 0;
-    if (t + 1 < ntiles) issue_rows(Y);
+    for (int st = 0; st < 4; ++st) s_ahead[st] = slot_at(tb + 2 * TILE + 16 * st + col);
+    issue_rows(Y);
+    // Keep the loads above the compute: the scheduler would otherwise sink them below it and
+    // expose their latency at the next step.
+    __builtin_amdgcn_sched_barrier(0);
     compute(t, X);
 #pragma unroll
     for (int st = 0; st < 4; ++st) X.s[st] = s_ahead[st];
