@@ -50,7 +50,7 @@ def parse():
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--kernel-reps", type=int, default=20, help="launches timed per layer for the roofline")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--eager", action="store_true", help="score each step eagerly (second K read)")
+    p.add_argument("--eager", action="store_true", help="score each step eagerly (second K pass per step)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="only run a plain device copy of this many MiB (5 launches): the byte-counter "
                         "calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE runs")
@@ -65,6 +65,13 @@ def decode_bytes(n_resident):
     2 B each) and the 64 bf16 sinks read once per sequence.
     """
     return n_resident * (HKV * D * 2 * 2 + HKV * 4 * 2 + 4) + HQ * D * 2 * 2 + HQ * 2
+
+
+def attention_bytes(n_resident):
+    """Algorithmic HBM bytes of the fused attention kernel for one (sequence, layer): K and V
+    rows and the slot index per key; q in, o out and the sinks. The score update is done by
+    the queue flush, so its bytes are not this kernel's."""
+    return n_resident * (HKV * D * 2 * 2 + 4) + HQ * D * 2 * 2 + HQ * 2
 
 
 def boundary_bytes(n_cols, width, count, freed, layers):
@@ -132,7 +139,7 @@ class Workload:
             kv_indptr=torch.zeros(bs + 2, dtype=torch.int32, device=dev))
         ge.STATE = None
         st = ge.state(self.backend)
-        st.lag = not args.eager
+        st.score_mode = "eager" if args.eager else "queue"
         self.st = st
         st.scores.uniform_(0.0, 1.0, generator=torch.Generator(device=dev).manual_seed(7))
         r2t = torch.zeros((bs + 1, width), dtype=torch.int32)
@@ -180,6 +187,7 @@ class Workload:
         st.table.copy_(table.to(dev))
         self.new_slots = torch.stack(self.new_slots).to(dev)  # [bs, steps]
         self.rows = torch.arange(1, bs + 1, device=dev)
+        self.rows_host = list(range(1, bs + 1))
         self.lens = list(lens)
         self.seq_lens = torch.tensor(lens, dtype=torch.int64, device=dev)
         cap = sum(r["count"] + r["len"] - r["frontier"] for r in rows) + bs * (total_steps + 2)
@@ -220,6 +228,7 @@ class Workload:
         self.seq_lens = lens_t + 1
         self.lens = [n + 1 for n in self.lens]
         bs = a.bs
+        ge.begin_decode_step(self.rows_host, st)  # flushes rows whose score queue is full
         ge.fill(self.backend, bs, self.seq_lens, self.rows, self.kv_indices)
         self.backend.forward_metadata = SimpleNamespace(kv_indptr=self.backend.kv_indptr[:bs + 1],
                                                         kv_indices=self.kv_indices)
@@ -247,7 +256,7 @@ def kernel_roofline(w, reps):
                          seq_lens_cpu=w.max_resident_list())
     # Resident counts of the last step (the CSR already in kv_indices).
     res = [w.resident(i) for i in range(bs)]
-    per_launch = sum(decode_bytes(r) for r in res)
+    per_launch = sum(attention_bytes(r) for r in res)
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps * a.layers)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps * a.layers)]
@@ -374,10 +383,10 @@ def main():
                                "budget 32768 (512+4096+28160), head_sum, evict every 64 steps, 16-token pages, "
                                "2% heavy hitters",
                    "batch": args.bs, "layers": args.layers, "budget": args.budget, "interval": args.interval,
-                   "policy": args.policy, "score_mode": "eager" if args.eager else "lag",
+                   "policy": args.policy, "score_mode": "eager" if args.eager else "queue",
                    "mean_resident": round(statistics.mean(w.resident_hist), 1),
                    "boundaries": w.boundaries, "wall_s": round(wall, 3)},
-        "roofline": {"bound": "hbm", "kernel": "decode_split_kernel+decode_merge_kernel (one layer, bs=32)",
+        "roofline": {"bound": "hbm", "kernel": "decode_fused_kernel+decode_merge_kernel (one layer, bs=32)",
                      "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": per_launch, "avg_launch_us": round(avg_us, 2)},

@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 GSE_OK = 0
 I32, I64 = 0, 1
 F32, BF16 = 0, 1
-SCORE_NONE, SCORE_EAGER, SCORE_LAG = 0, 1, 2
+SCORE_NONE, SCORE_EAGER, SCORE_QUEUE = 0, 1, 2
 POLICY_IDS = {"head_sum_2048": 1, "head_max_sum_2048": 2, "random_2048": 3,
               "random_reservoir_2048": 4, "prefix_sliding_2048": 5}
 BOUNDARY_EVICTED, BOUNDARY_DEFERRED, BOUNDARY_ERR_HEADS, BOUNDARY_ERR_SWA, BOUNDARY_ERR_PACKED = 0, 2, 3, 4, 5
@@ -30,13 +30,13 @@ SIGNATURES = {
     "gse_last_error": (ctypes.c_char_p, []),
     "gse_fill": (_i, [_p, _l, _p, _l, _p, _i, _p, _i, _p, _p, _i, _p, _p, _i, _p]),
     "gse_zero_slots": (_i, [_p, _i, _l, _i, _l, _l, _p, _i, _l, _p]),
-    "gse_decode_workspace_bytes": (_l, [_i, _i, _i, _i]),
+    "gse_decode_workspace_bytes": (_l, [_i, _i, _i]),
     "gse_decode": (_i, [_p, _l, _l, _p, _p, _l, _l, _p, _p, _i, _p, _i, _p, _p, _i, _p, _l, _l, _p, _l, _l, _p,
-                        _p, _p, _p, _i, _i, _i, _i, _f, _i, _i, _i, _p, _l, _p]),
-    "gse_decode_flush": (_i, [_p, _l, _l, _p, _l, _p, _l, _l, _p, _p, _p, _p, _i, _i, _p, _l, _l, _p, _p, _p,
-                              _i, _i, _i, _f, _i, _i, _p]),
+                        _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _i, _i, _p, _l, _p]),
+    "gse_score_flush": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p, _p,
+                             _p, _p, _i, _i, _i, _i, _i, _f, _p]),
     "gse_decode_scores_from_lse": (_i, [_p, _l, _l, _p, _l, _l, _p, _p, _i, _p, _l, _l, _p, _i, _i, _p, _i,
-                                        _p, _p, _i, _p, _l, _l, _i, _i, _i, _i, _f, _i, _i, _p, _l, _p]),
+                                        _p, _p, _i, _p, _l, _l, _i, _i, _i, _i, _f, _i, _p, _l, _p]),
     "gse_reservoir_scores": (_i, [_p, _i, _p, _p, _i, _i, _l, _l, _p, _p]),
     "gse_select_kept": (_i, [_p, _p, _i, _i, _l, _l, _l, _l, _l, _l, _i, _i, _p, _p, _p, _l, _p]),
     "gse_boundary_workspace_bytes": (_l, [_i, _i, _i, _l, _l, _l]),

@@ -47,10 +47,11 @@ enum {
 
 /* Decode score modes of gse_decode. */
 enum {
-  GSE_SCORE_NONE = 0,  /* attention only                                               */
-  GSE_SCORE_EAGER = 1, /* this step's scores are added before the call returns          */
-  GSE_SCORE_LAG = 2    /* the previous step's scores are added while K streams for this  */
-                       /* step; this step's are left pending (see gse_decode_flush)      */
+  GSE_SCORE_NONE = 0,  /* attention only                                                */
+  GSE_SCORE_EAGER = 1, /* this step's scores are added before the call returns (second K */
+                       /* pass, the reference's per-step update)                         */
+  GSE_SCORE_QUEUE = 2  /* this step's query is queued; gse_score_flush adds the queued   */
+                       /* queries' scores (one K pass per queue)                         */
 };
 
 /* Boundary outcome written to device memory by gse_boundary. */
@@ -96,25 +97,29 @@ int gse_fill(const int32_t* table, int64_t table_stride, const int32_t* req_to_t
 int gse_zero_slots(float* scores, int layers, int64_t layer_stride, int kv_heads, int64_t head_stride,
                    int64_t slot_stride, const void* slots, int slots_dtype, int64_t n, gse_stream_t stream);
 
-/* Workspace bytes gse_decode / gse_decode_scores_from_lse need for bs sequences and max_splits splits. */
-int64_t gse_decode_workspace_bytes(int bs, int max_splits, int q_heads, int head_dim);
+/* Workspace bytes gse_decode needs for bs sequences. */
+int64_t gse_decode_workspace_bytes(int bs, int q_heads, int head_dim);
 
 /*
- * decode — one full-attention layer's decode step: split-KV attention with the
- * learned sink folded into the softmax normaliser, fused with the per-KV-head
- * H2O score update. Replaces SGLang's decode_attention_fwd (the attention of
- * R:203-224's caller, O:35-41) together with `_decode_scores` / `after_decode`
- * (R:155-224).
- *   o[b, h]      = sum_s softmax([q_h.k_s*scale, sink_h])_s v_s  (sink column dropped)
- *   norm_out[b,h] = log(exp(sink_h) + sum_s exp(q_h.k_s*scale))
- *   scores[g, slot_s] += sum_{h in g} p_hs   (mode 1)  or  max_{h in g} p_hs  (mode 2)
+ * decode — one full-attention layer's decode step: attention with the learned
+ * sink folded into the softmax normaliser, plus the H2O score of the step's
+ * query. Replaces SGLang's decode_attention_fwd (the attention before the
+ * reference's after_decode hook, O:35-41) together with `_decode_scores` /
+ * `after_decode` (R:155-224):
+ *   o[b, h]       = sum_s softmax([q_h.k_s*scale, sink_h])_s v_s  (sink column dropped)
+ *   norm_out[b,h] = log(exp(sink_h) + sum_s exp(q_h.k_s*scale))    (may be null)
+ *   scores[g, slot_s] += sum_{h in g} p_hs  (mode 1)  or  max_{h in g} p_hs  (mode 2)
  * where mode = mode_by_row[rows[b]]; rows whose mode is not 1 or 2 get no score.
- * score_mode selects GSE_SCORE_NONE / _EAGER / _LAG. In LAG mode the kernel
- * adds the scores of the query left pending in (pend_q, pend_norm, pend_len) for
- * this layer by the previous call while it streams K for this call, then leaves
- * this call's query pending; the pending rows' slot lists must be prefixes of
- * this call's lists (true between boundaries). Shapes: q_heads = 8 * kv_heads,
- * kv_heads <= 8, head_dim = 64. Fixed grid (max_splits x bs): capturable.
+ * score_mode GSE_SCORE_EAGER adds the scores before returning (max_len bounds
+ * every sequence's list length); GSE_SCORE_QUEUE appends the step to the row's
+ * queue instead: queue_count[row] = n + 1 for n = queue_count[row], and if n < queue_cap
+ *   entry n receives queue_q[row, n] = q[b] ([q_heads, 64] bf16), queue_norm[row, n] =
+ *   norm (natural log, [q_heads]) and queue_lim[row, n] = the list length;
+ * gse_score_flush adds the queued scores. The caller flushes a row before its queue is
+ * full (a count above queue_cap records dropped steps) and before the row's list changes
+ * other than by appending (boundaries). Shapes: q_heads = 8 * kv_heads, kv_heads <= 8,
+ * head_dim = 64. The attention kernel runs one workgroup per CU over an equal share of
+ * the batch's keys; fixed grid, no host reads: capturable in a HIP graph.
  */
 int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
@@ -122,25 +127,29 @@ int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                const void* sinks, int sinks_dtype, const int32_t* mode_by_row, const void* rows, int rows_dtype,
                float* scores, int64_t scores_stride_g, int64_t scores_stride_s,
                void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
-               void* pend_q, float* pend_norm, int32_t* pend_len,
-               int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int chunk, int max_splits,
+               void* queue_q, float* queue_norm, int32_t* queue_lim, int32_t* queue_count, int queue_cap,
+               int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int max_len,
                int score_mode, void* workspace, int64_t workspace_bytes, gse_stream_t stream);
 
 /*
- * decode_flush — add the pending (LAG mode) scores of the listed rows of one
- * layer and clear them. The slot list of a pending row is rebuilt from the
- * eviction state as in `fill`: table[row, :count] ++ req_to_token[row, frontier:],
- * truncated to pend_len[row]. No reference counterpart: the reference adds
- * scores eagerly (R:218-224); this restores the same scores before they are read.
+ * score_flush — add the queued decode scores of the listed rows, for every full
+ * layer, and empty their queues. No reference counterpart as an entry point: the
+ * reference adds each step's scores eagerly (R:189-200, R:218-224); this applies
+ * the same update for all queued steps at once:
+ *   scores[l, g, slot(c)] += sum_i [c < lim_i] (sum | max)_{h in g} exp(q_ih . k_cg * scale - norm_ih)
+ * with slot(c) = table[row, c] for c < count[row], else req_to_token[row, frontier[row] + c - count[row]]
+ * (the list of `fill`). k_pools is a device array of `layers` pointers; the queue
+ * buffers are those of gse_decode for layer 0, each layer's `rows_total` rows after
+ * the previous layer's. max_len bounds every listed row's list length.
  */
-int gse_decode_flush(const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_h,
-                     const int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
-                     int64_t r2t_width, const int32_t* frontier, const int32_t* count, const int32_t* mode_by_row,
-                     const void* rows, int rows_dtype, int n_rows,
-                     float* scores, int64_t scores_stride_g, int64_t scores_stride_s,
-                     void* pend_q, float* pend_norm, int32_t* pend_len,
-                     int q_heads, int kv_heads, int head_dim, float sm_scale, int chunk, int max_splits,
-                     gse_stream_t stream);
+int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                    float* scores, int64_t scores_stride_l, int64_t scores_stride_g, int64_t scores_stride_s,
+                    const int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
+                    const int32_t* frontier, const int32_t* count, const int32_t* mode_by_row,
+                    const void* rows, int rows_dtype, int n_rows, int64_t max_len,
+                    const void* queue_q, const float* queue_norm, const int32_t* queue_lim, int32_t* queue_count,
+                    int rows_total, int queue_cap, int q_heads, int kv_heads, int head_dim, float sm_scale,
+                    gse_stream_t stream);
 
 /*
  * decode_scores_from_lse — the reference's score update given an external
@@ -149,6 +158,7 @@ int gse_decode_flush(const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_
  * max_kv_splits] (strides in elements) over the valid splits of SGLang's layout
  * per = cdiv(cdiv(len, num_kv_splits[b]), min_block_kv) * min_block_kv, started
  * at (sink, 1) (R:180-188), then every resident key's probability is added.
+ * max_len bounds every sequence's list length; workspace holds bs * q_heads floats.
  */
 int gse_decode_scores_from_lse(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_h,
@@ -159,7 +169,7 @@ int gse_decode_scores_from_lse(const void* q, int64_t q_stride_b, int64_t q_stri
                                const void* rows, int rows_dtype, float* scores, int64_t scores_stride_g,
                                int64_t scores_stride_s,
                                int bs, int q_heads, int kv_heads, int head_dim, float sm_scale,
-                               int chunk, int max_splits, void* workspace, int64_t workspace_bytes,
+                               int max_len, void* workspace, int64_t workspace_bytes,
                                gse_stream_t stream);
 
 /*

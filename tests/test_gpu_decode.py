@@ -101,7 +101,7 @@ def _oracle_step(b, st, q, sinks, perm, indptr, lid, mode):
 def test_fused_decode_matches_oracle(mode, lag):
     lengths = [37, 1500, 3001]
     b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths)
-    st.lag = lag
+    st.score_mode = "queue" if lag else "eager"
     st.mode[:] = mode
     b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=perm)
     fb = SimpleNamespace(out_cache_loc=torch.zeros(3, dtype=torch.int64, device="cuda"), req_pool_indices=rows,
@@ -109,7 +109,7 @@ def test_fused_decode_matches_oracle(mode, lag):
     o = torch.empty_like(q)
     assert ge.decode(b, q.reshape(3, -1), layer(1), fb, sinks, o.reshape(3, -1))
     if lag:
-        assert float(st.scores.abs().sum()) == 0.0  # the update is pending until flushed
+        assert float(st.scores.abs().sum()) == 0.0  # the step is queued until flushed
         # The flush rebuilds each row's list from the eviction state (empty table, tail = req_to_token).
         for i, r in enumerate(rows.tolist()):
             st.req_to_token[r, :lengths[i]] = perm[indptr[i]:indptr[i + 1]].int()
@@ -124,15 +124,15 @@ def test_fused_decode_matches_oracle(mode, lag):
     torch.testing.assert_close(st.scores, expected, rtol=2e-3, atol=1e-6)
 
 
-def test_lag_over_steps_equals_eager():
-    """Several decode steps with growing lists: lagged + flushed scores equal eager ones."""
+def test_queue_over_steps_equals_eager():
+    """Several decode steps with growing lists: queued + flushed scores equal eager ones."""
     g = torch.Generator().manual_seed(3)
     results = {}
     for lag in (False, True):
         ge.STATE = None
         b = backend(gen=torch.Generator().manual_seed(1))
         st = ge.state(b)
-        st.lag = lag
+        st.score_mode = "queue" if lag else "eager"
         st.mode[:] = 1
         base = [100, 700]
         perm = (torch.randperm(19999, generator=torch.Generator().manual_seed(2))[:2000] + 1).cuda()
@@ -153,7 +153,8 @@ def test_lag_over_steps_equals_eager():
         st.req_to_token[2, :base[1] + 3] = perm[1000:1000 + base[1] + 3].int()
         ge.flush(st)
         results[lag] = st.scores.clone()
-    torch.testing.assert_close(results[True], results[False], rtol=1e-6, atol=1e-9)
+    # Only the fp32 summation order differs (per step vs per queue).
+    torch.testing.assert_close(results[True], results[False], rtol=1e-5, atol=1e-8)
 
 
 @pytest.mark.parametrize("mode", [1, 2])
@@ -189,7 +190,7 @@ def test_rows_without_a_policy_get_no_scores_and_sliding_layers_are_skipped():
     b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths, seed=6)
     st.mode[:] = 0
     st.mode[2] = 2
-    st.lag = False
+    st.score_mode = "eager"
     b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=perm)
     fb = SimpleNamespace(out_cache_loc=torch.zeros(2, dtype=torch.int64, device="cuda"), req_pool_indices=rows,
                          seq_lens_cpu=torch.tensor(lengths))
@@ -201,3 +202,44 @@ def test_rows_without_a_policy_get_no_scores_and_sliding_layers_are_skipped():
     assert not bool(touched[perm[:64]].any())
     assert bool(touched[perm[64:]].all())
     assert float(st.scores[0].abs().sum()) == 0.0
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_full_queues_flush_before_the_step(monkeypatch, mode):
+    """More steps than the queue holds: begin_decode_step flushes full queues, so queued +
+    flushed scores equal the eager per-step update (head-sum and head-max)."""
+    monkeypatch.setenv("GSTAR_EVICT_QUEUE", "3")
+    results = {}
+    steps, base = 8, [130, 900]
+    perm = (torch.randperm(19999, generator=torch.Generator().manual_seed(12))[:2000] + 1).cuda()
+    qs = [torch.randn((2, 64, 64), generator=torch.Generator().manual_seed(40 + t)).to(torch.bfloat16).cuda()
+          for t in range(steps)]
+    sinks = torch.randn(64, generator=torch.Generator().manual_seed(7)).cuda()
+    for score_mode in ("eager", "queue"):
+        ge.STATE = None
+        b = backend(gen=torch.Generator().manual_seed(9))
+        st = ge.state(b)
+        assert st.queue_cap == 3
+        st.score_mode = score_mode
+        for r in (1, 2):
+            st.entries[r] = {"mode": mode}
+            st.mode[r] = mode
+        st.req_to_token[1, :base[0] + steps] = perm[:base[0] + steps].int()
+        st.req_to_token[2, :base[1] + steps] = perm[1000:1000 + base[1] + steps].int()
+        for t in range(steps):
+            lens = [base[0] + t, base[1] + t]
+            idx = torch.cat((perm[:lens[0]], perm[1000:1000 + lens[1]]))
+            indptr = torch.tensor([0, lens[0], lens[0] + lens[1]], dtype=torch.int32, device="cuda")
+            b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=idx)
+            fb = SimpleNamespace(out_cache_loc=idx[indptr[1:].long() - 1], req_pool_indices=torch.tensor(
+                [1, 2], device="cuda"), seq_lens_cpu=torch.tensor(lens))
+            ge.begin_decode_step([1, 2], st)
+            if score_mode == "queue":
+                assert max(st.queued.values()) <= st.queue_cap
+            o = torch.empty((2, 64, 64), dtype=torch.bfloat16, device="cuda")
+            ge.decode(b, qs[t].reshape(2, -1), layer(1), fb, sinks, o.reshape(2, -1))
+        assert int(st.qcount.max()) <= st.queue_cap  # no step was dropped
+        ge.flush(st)
+        assert int(st.qcount.abs().sum()) == 0
+        results[score_mode] = st.scores.clone()
+    torch.testing.assert_close(results["queue"], results["eager"], rtol=1e-5, atol=1e-8)
