@@ -321,6 +321,18 @@ def cpu_baseline(w):
                       f"{rate:.2f} boundaries/step"}
 
 
+def measured_traffic():
+    """HBM bytes per fused decode launch from the committed rocprofv3 summary (FETCH_SIZE and
+    WRITE_SIZE of the same workload, scaled by a copy kernel's counts), or None."""
+    path = os.path.join(ROOT, "profiles", "decode_fused_kernel_bs32_32K.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("hbm_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def copy_calibration(torch, mib):
     """A plain device-to-device copy of `mib` MiB, five times, timed with events."""
     n = mib * (1 << 20)
@@ -370,10 +382,7 @@ def main():
     gbs = w.bytes / (gpu_ms / 1000) / 1e9
     per_launch, avg_us = kernel_roofline(w, args.kernel_reps)
     achieved = per_launch / (avg_us * 1e-6) / 1e9
-    traffic = None
-    pmc = os.path.join(ROOT, "profiles", "decode_traffic.json")
-    if os.path.exists(pmc):
-        traffic = json.load(open(pmc)).get("hbm_bytes_per_launch")
+    traffic = measured_traffic()
     result = {
         "metric": "fused attn+score+evict µs/decode-step & HBM GB/s (% peak), bs=32, 32K budget",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
