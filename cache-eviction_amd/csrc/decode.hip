@@ -282,7 +282,7 @@ struct MergeArgs {
 };
 
 // Grid (bs): thread (head t/8, dims [8*(t%8), +8)) merges the partials of its head with
-// the sink: o = sum_w 2^(m_w - M) o_w / (2^(sink - M) + sum_w 2^(m_w - M) l_w).
+// the sink: o = sum_w 2^(m_w - M) o_w / (2^(sink - M) + sum_w 2^(m_w - M) l_w), M the maximum.
 __global__ __launch_bounds__(512) void decode_merge_kernel(MergeArgs a) {
   const int b = blockIdx.x;
   const int h = threadIdx.x >> 3;
@@ -307,17 +307,32 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(MergeArgs a) {
     wf = start / C;
     wl = (end - 1) / C;
   }
-  const float sink2 = load_float_dyn(a.sinks, a.sinks_dtype, h) * kLog2e;
-  float mx = sink2;
-  for (int w = wf; w <= wl; ++w) mx = fmaxf(mx, a.part[((int64_t(w) + b) * a.q_heads + h) * PART + D]);
-  float lsum = fast_exp2(sink2 - mx);
+  // Online merge from the sink's state (m = sink, l = 1, o = 0), four partials per batch with
+  // their loads issued together (a partial past the range is read again with weight 0).
+  float mx = load_float_dyn(a.sinks, a.sinks_dtype, h) * kLog2e;
+  float lsum = 1.f;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  for (int w = wf; w <= wl; ++w) {
-    const float* ps = a.part + ((int64_t(w) + b) * a.q_heads + h) * PART;
-    const float wt = fast_exp2(ps[D] - mx);
-    lsum += wt * ps[D + 1];
-    acc0 += wt * *reinterpret_cast<const f32x4_t*>(ps + 8 * j);
-    acc1 += wt * *reinterpret_cast<const f32x4_t*>(ps + 8 * j + 4);
+  for (int w0 = wf; w0 <= wl; w0 += 4) {
+    float pm[4], pl[4];
+    f32x4_t po0[4], po1[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int w = w0 + k <= wl ? w0 + k : wl;
+      const float* ps = a.part + ((int64_t(w) + b) * a.q_heads + h) * PART;
+      pm[k] = w0 + k <= wl ? ps[D] : -INFINITY;
+      pl[k] = ps[D + 1];
+      po0[k] = *reinterpret_cast<const f32x4_t*>(ps + 8 * j);
+      po1[k] = *reinterpret_cast<const f32x4_t*>(ps + 8 * j + 4);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float m_new = fmaxf(mx, pm[k]);
+      const float so = fast_exp2(mx - m_new), sk = fast_exp2(pm[k] - m_new);
+      lsum = lsum * so + pl[k] * sk;
+      acc0 = acc0 * so + po0[k] * sk;
+      acc1 = acc1 * so + po1[k] * sk;
+      mx = m_new;
+    }
   }
   const float inv = 1.f / lsum;
   uint4 out;

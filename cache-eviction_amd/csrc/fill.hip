@@ -25,8 +25,11 @@ GSE_DEVICE int64_t fill_size(const FillArgs& a, int i) {
   return load_index_dyn(a.lens, a.lens_dtype, i) - a.frontier[row] + a.count[row];
 }
 
-// One workgroup per batch entry: its offset is the sum of the sizes before it
-// (reduced in the workgroup), then the table part and the tail are copied.
+// Grid (bs, segments of FILL_SEG entries): each workgroup finds its entry's CSR offset (the
+// sum of the sizes before it, reduced in the workgroup) and copies one segment of the
+// entry's list (table part, then tail); workgroups past the entry's list only exit.
+constexpr int FILL_SEG = 2048;
+
 template <typename OutT>
 __global__ __launch_bounds__(256) void fill_kernel(FillArgs a) {
   __shared__ int64_t red[256];
@@ -43,16 +46,17 @@ __global__ __launch_bounds__(256) void fill_kernel(FillArgs a) {
   const int64_t row = load_index_dyn(a.rows, a.rows_dtype, b);
   const int64_t cnt = a.count[row];
   const int64_t fr = a.frontier[row];
-  const int64_t tail = load_index_dyn(a.lens, a.lens_dtype, b) - fr;
-  if (threadIdx.x == 0) {
-    a.indptr[b + 1] = int32_t(start + cnt + tail);
+  const int64_t total = cnt + load_index_dyn(a.lens, a.lens_dtype, b) - fr;
+  if (blockIdx.y == 0 && threadIdx.x == 0) {
+    a.indptr[b + 1] = int32_t(start + total);
     if (b == 0) a.indptr[0] = 0;
   }
+  const int64_t lo = int64_t(blockIdx.y) * FILL_SEG;
+  const int64_t hi = lo + FILL_SEG < total ? lo + FILL_SEG : total;
   OutT* out = static_cast<OutT*>(a.indices) + start;
   const int32_t* trow = a.table + row * a.table_stride;
-  for (int64_t i = threadIdx.x; i < cnt; i += blockDim.x) out[i] = OutT(trow[i]);
-  const int32_t* rrow = a.r2t + row * a.r2t_stride + fr;
-  for (int64_t i = threadIdx.x; i < tail; i += blockDim.x) out[cnt + i] = OutT(rrow[i]);
+  const int32_t* rrow = a.r2t + row * a.r2t_stride + fr - cnt;  // entry i >= cnt is rrow[i]
+  for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) out[i] = OutT(i < cnt ? trow[i] : rrow[i]);
 }
 
 template <typename SlotT>
@@ -72,19 +76,21 @@ using namespace gse;
 
 extern "C" int gse_fill(const int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
                         const void* rows, int rows_dtype, const void* seq_lens, int lens_dtype,
-                        const int32_t* frontier, const int32_t* count, int bs, int32_t* kv_indptr,
-                        void* kv_indices, int indices_dtype, gse_stream_t stream) {
+                        const int32_t* frontier, const int32_t* count, int bs, int64_t max_len,
+                        int32_t* kv_indptr, void* kv_indices, int indices_dtype, gse_stream_t stream) {
   if (bs < 0) return gse_fail(GSE_EINVAL, "fill: bs < 0");
   if (bs == 0) return GSE_OK;
   if (!table || !req_to_token || !rows || !seq_lens || !frontier || !count || !kv_indptr || !kv_indices)
     return gse_fail(GSE_EINVAL, "fill: null pointer");
   FillArgs a = {table, table_stride, req_to_token, r2t_stride, rows, rows_dtype, seq_lens, lens_dtype,
                 frontier, count, bs, kv_indptr, kv_indices};
+  if (max_len < 0) return gse_fail(GSE_EINVAL, "fill: max_len < 0");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(bs), static_cast<uint32_t>((max_len + FILL_SEG - 1) / FILL_SEG + 1));
   if (indices_dtype == GSE_I64)
-    hipLaunchKernelGGL(fill_kernel<int64_t>, dim3(bs), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(fill_kernel<int64_t>, grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL(fill_kernel<int32_t>, dim3(bs), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(fill_kernel<int32_t>, grid, dim3(256), 0, s, a);
   return gse_launch_check("fill");
 }
 

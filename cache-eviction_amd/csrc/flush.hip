@@ -167,13 +167,16 @@ __global__ __launch_bounds__(256) void score_flush_kernel(FlushArgs a) {
   }
 }
 
-// The queues of the flushed (layer, row) pairs are empty afterwards.
-__global__ void flush_clear_kernel(const void* rows, int rows_dtype, int n_rows, int layers, int rows_total,
-                                   int32_t* pcount) {
+// The queues of the flushed (layer, row) pairs are empty afterwards; a count above the
+// capacity (steps the decode merge could not queue) sets *overflow.
+__global__ void flush_clear_kernel(const void* rows, int rows_dtype, int n_rows, int layers, int rows_total, int cap,
+                                   int32_t* pcount, int32_t* overflow) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n_rows * layers) return;
   const int l = i / n_rows;
-  pcount[int64_t(l) * rows_total + load_index_dyn(rows, rows_dtype, i % n_rows)] = 0;
+  int32_t* c = pcount + int64_t(l) * rows_total + load_index_dyn(rows, rows_dtype, i % n_rows);
+  if (overflow && *c > cap) *overflow = 1;
+  *c = 0;
 }
 
 }  // namespace gse
@@ -187,7 +190,8 @@ extern "C" int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stri
                                const int32_t* count, const int32_t* mode_by_row, const void* rows, int rows_dtype,
                                int n_rows, int64_t max_len, const void* pend_q, const float* pend_norm,
                                const int32_t* pend_lim, int32_t* pend_count, int rows_total, int queue_cap,
-                               int q_heads, int kv_heads, int head_dim, float sm_scale, gse_stream_t stream) {
+                               int q_heads, int kv_heads, int head_dim, float sm_scale, int32_t* overflow,
+                               gse_stream_t stream) {
   using namespace fl;
   if (head_dim != D || kv_heads < 1 || kv_heads > 8 || q_heads != GROUP * kv_heads)
     return gse_fail(GSE_ESHAPE, "score_flush: need head_dim 64 and q_heads == 8 * kv_heads <= 64");
@@ -212,6 +216,6 @@ extern "C" int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stri
   }
   const int total = n_rows * layers;
   hipLaunchKernelGGL(flush_clear_kernel, dim3((total + 255) / 256), dim3(256), 0, s, rows, rows_dtype, n_rows, layers,
-                     rows_total, pend_count);
+                     rows_total, queue_cap, pend_count, overflow);
   return gse_launch_check("score_flush clear");
 }

@@ -28,13 +28,13 @@ _p, _i, _l, _f, _d = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_flo
 SIGNATURES = {
     "gse_version": (_i, []),
     "gse_last_error": (ctypes.c_char_p, []),
-    "gse_fill": (_i, [_p, _l, _p, _l, _p, _i, _p, _i, _p, _p, _i, _p, _p, _i, _p]),
+    "gse_fill": (_i, [_p, _l, _p, _l, _p, _i, _p, _i, _p, _p, _i, _l, _p, _p, _i, _p]),
     "gse_zero_slots": (_i, [_p, _i, _l, _i, _l, _l, _p, _i, _l, _p]),
     "gse_decode_workspace_bytes": (_l, [_i, _i, _i]),
     "gse_decode": (_i, [_p, _l, _l, _p, _p, _l, _l, _p, _p, _i, _p, _i, _p, _p, _i, _p, _l, _l, _p, _l, _l, _p,
                         _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _i, _i, _p, _l, _p]),
     "gse_score_flush": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p, _p,
-                             _p, _p, _i, _i, _i, _i, _i, _f, _p]),
+                             _p, _p, _i, _i, _i, _i, _i, _f, _p, _p]),
     "gse_decode_scores_from_lse": (_i, [_p, _l, _l, _p, _l, _l, _p, _p, _i, _p, _l, _l, _p, _i, _i, _p, _i,
                                         _p, _p, _i, _p, _l, _l, _i, _i, _i, _i, _f, _i, _p, _l, _p]),
     "gse_reservoir_scores": (_i, [_p, _i, _p, _p, _i, _i, _l, _l, _p, _p]),

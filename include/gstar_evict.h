@@ -83,11 +83,12 @@ const char* gse_last_error(void);
  * SGLang's create_flashinfer_kv_indices_triton called twice, R:147-151):
  *   kv_indptr[b+1] = sum_{i<=b} (seq_lens[i] - frontier[rows[i]] + count[rows[i]])
  *   kv_indices     = table[row, :count] ++ req_to_token[row, frontier:seq_len]   per b
- * Fixed grid (bs workgroups), no host reads: capturable in a HIP graph.
+ * max_len bounds every entry's list length (e.g. req_to_token's width); the grid is
+ * (bs, max_len / 2048 + 1) and reads nothing on the host: capturable in a HIP graph.
  */
 int gse_fill(const int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
              const void* rows, int rows_dtype, const void* seq_lens, int lens_dtype,
-             const int32_t* frontier, const int32_t* count, int bs,
+             const int32_t* frontier, const int32_t* count, int bs, int64_t max_len,
              int32_t* kv_indptr, void* kv_indices, int indices_dtype, gse_stream_t stream);
 
 /*
@@ -140,7 +141,8 @@ int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * with slot(c) = table[row, c] for c < count[row], else req_to_token[row, frontier[row] + c - count[row]]
  * (the list of `fill`). k_pools is a device array of `layers` pointers; the queue
  * buffers are those of gse_decode for layer 0, each layer's `rows_total` rows after
- * the previous layer's. max_len bounds every listed row's list length.
+ * the previous layer's. max_len bounds every listed row's list length. If a flushed
+ * count exceeds queue_cap (steps that were dropped), *overflow (may be null) is set to 1.
  */
 int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
                     float* scores, int64_t scores_stride_l, int64_t scores_stride_g, int64_t scores_stride_s,
@@ -149,7 +151,7 @@ int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stride_s, int64
                     const void* rows, int rows_dtype, int n_rows, int64_t max_len,
                     const void* queue_q, const float* queue_norm, const int32_t* queue_lim, int32_t* queue_count,
                     int rows_total, int queue_cap, int q_heads, int kv_heads, int head_dim, float sm_scale,
-                    gse_stream_t stream);
+                    int32_t* overflow, gse_stream_t stream);
 
 /*
  * decode_scores_from_lse — the reference's score update given an external

@@ -60,9 +60,9 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     rc = lib.gse_decode(None, 0, 0, None, None, 0, 0, None, None, 0, None, 0, None, None, 0, None, 0, 1, None, 0, 0,
                         None, None, None, None, None, 0, 4, 64, 8, 128, 0.125, 512, 0, None, 0, None)
     assert rc != 0 and b"head_dim" in lib.gse_last_error()
-    rc = lib.gse_fill(None, 0, None, 0, None, 0, None, 0, None, None, -1, None, None, 0, None)
+    rc = lib.gse_fill(None, 0, None, 0, None, 0, None, 0, None, None, -1, 0, None, None, 0, None)
     assert rc != 0
-    assert lib.gse_fill(None, 0, None, 0, None, 0, None, 0, None, None, 0, None, None, 0, None) == 0
+    assert lib.gse_fill(None, 0, None, 0, None, 0, None, 0, None, None, 0, 0, None, None, 0, None) == 0
     rc = lib.gse_score_flush(None, 12, 512, 64, None, 0, 0, 0, None, 0, None, 0, None, None, None, None, 0, 1, 100,
-                             None, None, None, None, 4, 65, 64, 8, 64, 0.125, None)
+                             None, None, None, None, 4, 65, 64, 8, 64, 0.125, None, None)
     assert rc != 0 and b"queue_cap" in lib.gse_last_error()
