@@ -304,6 +304,308 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
   }
 }
 
+// ------------------------------------------------- LDS-resident selection --
+//
+// Boundary-mode selection for rows of at most SEL_LDS_KEYS columns: the high 32
+// bits of every column's ordering key stay in LDS for all radix passes. The key
+// of an unprotected column is (hi, lo, position) compared as a 96-bit number: for
+// fp32 table scores hi = the ordered fp32 bits and lo = 0; for float64 scores
+// (reservoir, random) hi:lo = the ordered float64 bits. Protected columns hold the
+// sentinel hi = 0, below every real key (scores are >= 0, so their ordered bits
+// are >= 0x80000000). lo and the position are recomputed from global memory, and
+// only for columns still tied with the threshold after the hi digits.
+constexpr int SEL_LDS_KEYS = 34816;  // 34 columns per thread
+
+GSE_DEVICE uint32_t ordered_f32(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+GSE_DEVICE int32_t col_pos(const SelArgs& a, int lg, int64_t c) {
+  return c < a.src.count ? a.src.pos_old[int64_t(lg) * a.src.pstride + c] : int32_t(a.src.frontier + c - a.src.count);
+}
+
+// 64-bit ordering key of an unprotected column (boundary-mode policies).
+GSE_DEVICE uint64_t col_key64(const SelArgs& a, int l, int g, int lg, int64_t c, int32_t p) {
+  if (a.src.policy == GSE_POLICY_RESERVOIR)
+    return ordered_f64(double(splitmix_bits(a.src.seed, l, g, p)) / 9007199254740992.0);
+  if (a.src.policy == GSE_POLICY_RANDOM) return ordered_f64(a.src.random_scores[int64_t(lg) * a.n_cols + c]);
+  if (a.src.policy == GSE_POLICY_PREFIX_SLIDING) return uint64_t(ordered_f32(0.f)) << 32;
+  const float sc = a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg + int64_t(a.src.slots[c]) * a.src.sss];
+  return uint64_t(ordered_f32(sc)) << 32;
+}
+
+// Digit j (0 = most significant) of the 96-bit composite (hi, lo, pos), 8 bits each.
+GSE_DEVICE uint32_t digit96(uint32_t hi, uint32_t lo, uint32_t pos, int j) {
+  const uint32_t w = j < 4 ? hi : (j < 8 ? lo : pos);
+  return (w >> (24 - 8 * (j & 3))) & 0xffu;
+}
+
+// Compare the top `digits` (0..4) bytes of x and y: -1, 0, +1.
+GSE_DEVICE int cmp_top(uint32_t x, uint32_t y, int digits) {
+  if (digits <= 0) return 0;
+  const int sh = 32 - 8 * (digits < 4 ? digits : 4);
+  const uint32_t a = sh >= 32 ? 0u : x >> sh, b = sh >= 32 ? 0u : y >> sh;
+  return a < b ? -1 : (a > b ? 1 : 0);
+}
+
+// Compare the first `fixed` digits of (hi, lo, pos) with the threshold prefix: -1, 0, +1.
+GSE_DEVICE int cmp96(uint32_t hi, uint32_t lo, uint32_t pos, uint32_t th, uint32_t tl, uint32_t tp, int fixed) {
+  int c = cmp_top(hi, th, fixed);
+  if (c != 0 || fixed <= 4) return c;
+  c = cmp_top(lo, tl, fixed - 4);
+  if (c != 0 || fixed <= 8) return c;
+  return cmp_top(pos, tp, fixed - 8);
+}
+
+__global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
+  constexpr int KPT = SEL_LDS_KEYS / SEL_THREADS;  // columns per thread: c = tid + k * SEL_THREADS
+  constexpr int BATCH = 17;                         // columns whose loads are issued together
+  static_assert(KPT % BATCH == 0, "whole batches");
+  __shared__ uint32_t keys[SEL_LDS_KEYS];  // hi key per column; later the position bitmap
+  __shared__ int hist[8][256];
+  __shared__ int tmp[128];
+  __shared__ int bcast[16];
+  __shared__ uint32_t kbits[SEL_LDS_KEYS / 32];  // kept-middle flag per column
+  __shared__ uint32_t redu[2][SEL_THREADS / 64];
+
+  const int lg = blockIdx.x;
+  const int l = lg / a.kv_heads, g = lg % a.kv_heads;
+  const int N = int(a.n_cols);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const bool f64 = a.src.policy == GSE_POLICY_RESERVOIR || a.src.policy == GSE_POLICY_RANDOM;
+  const bool table_scores = !f64 && !a.prefix_sliding;
+  auto col = [&](int k) { return int(threadIdx.x) + k * SEL_THREADS; };
+
+  // Positions of a batch of this thread's columns, all loads issued before any is used.
+  const int cnt = int(a.src.count);
+  const int32_t* prow = (a.src.pos_old && cnt > 0) ? a.src.pos_old + int64_t(lg) * a.src.pstride : nullptr;
+  auto load_pos = [&](int k0, int32_t* pb) {
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = col(k0 + u);
+      const int32_t v = prow ? prow[c < cnt ? c : cnt - 1] : 0;
+      pb[u] = c < cnt ? v : int32_t(a.src.frontier + c - cnt);
+    }
+  };
+
+  // Phase 1: hi keys, protection count, common high bits of the unprotected keys.
+  int nprot = 0;
+  uint32_t kand = 0xffffffffu, kor = 0u;
+  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
+    int32_t pb[BATCH];
+    load_pos(k0, pb);
+    float sc[BATCH];
+    if (table_scores) {
+      int32_t sl[BATCH];
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const int c = col(k0 + u);
+        sl[u] = a.src.slots[c < N ? c : N - 1];
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u)
+        sc[u] = a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg + int64_t(sl[u]) * a.src.sss];
+    }
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = col(k0 + u);
+      if (c < N) {
+        const bool prot = is_protected(a, pb[u]);
+        uint32_t hi = 0;
+        if (!prot) {
+          hi = table_scores ? ordered_f32(sc[u])
+                            : (a.prefix_sliding ? ordered_f32(0.f) : uint32_t(col_key64(a, l, g, lg, c, pb[u]) >> 32));
+          kand &= hi;
+          kor |= hi;
+        }
+        nprot += prot;
+        keys[c] = hi;
+      }
+    }
+  }
+  // Block AND / OR of the unprotected hi keys.
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    kand &= __shfl_xor(kand, o, 64);
+    kor |= __shfl_xor(kor, o, 64);
+  }
+  if (lane == 0) {
+    redu[0][wave] = kand;
+    redu[1][wave] = kor;
+  }
+  const int P = block_sum(nprot, tmp);  // synchronises the workgroup
+  kand = 0xffffffffu;
+  kor = 0u;
+  for (int w = 0; w < SEL_THREADS / 64; ++w) {
+    kand &= redu[0][w];
+    kor |= redu[1][w];
+  }
+  if (threadIdx.x == 0) a.prot_count[lg] = P;
+  const int M = N - P;
+  int k = a.prefix_sliding ? 0 : int(a.budget) - P;
+  if (k < 0) k = 0;  // deferred: keep nothing beyond the protected set
+  if (k > M) k = M;
+
+  // Phase 2: radix select of the k-th largest composite among unprotected columns. Leading
+  // hi digits shared by every unprotected key are fixed at once; the lo digits are all 0 for
+  // fp32 keys and are skipped. Each wave pair counts into its own histogram copy.
+  uint32_t th = 0, tl = 0, tp = 0;
+  int fixed = 0;
+  const bool take_all = (k == M);
+  int krem = k;
+  if (k > 0 && !take_all) {
+    const uint32_t diff = kand ^ kor;
+    const int common = diff ? __clz(diff) / 8 : 4;  // leading hi bytes equal for all
+    th = kand & (common >= 4 ? 0xffffffffu : ~(0xffffffffu >> (8 * common)));
+    fixed = common;
+    for (int j = common; j < 12; ++j) {
+      if (j >= 4 && j < 8 && !f64) {  // lo = 0 for every fp32 key
+        fixed = j + 1;
+        continue;
+      }
+      for (int i = threadIdx.x; i < 8 * 256; i += SEL_THREADS) (&hist[0][0])[i] = 0;
+      __syncthreads();
+      int* h = hist[wave & 7];
+      for (int c = threadIdx.x; c < N; c += SEL_THREADS) {
+        const uint32_t hi = keys[c];
+        if (hi == 0) continue;  // protected
+        if (j < 4) {
+          if (cmp96(hi, 0, 0, th, tl, tp, j) != 0) continue;
+          atomicAdd(&h[digit96(hi, 0, 0, j)], 1);
+        } else {
+          if (hi != th) continue;  // ties of the hi key: lo and position from memory
+          const int32_t p = col_pos(a, lg, c);
+          const uint32_t lo = f64 ? uint32_t(col_key64(a, l, g, lg, c, p)) : 0u;
+          if (cmp96(hi, lo, uint32_t(p), th, tl, tp, j) != 0) continue;
+          atomicAdd(&h[digit96(hi, lo, uint32_t(p), j)], 1);
+        }
+      }
+      __syncthreads();
+      if (threadIdx.x < 64) {
+        // Suffix sums over bins (lane owns bins 4*lane .. 4*lane + 3): find the bin where the
+        // krem-th largest falls.
+        int cnt[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          int v = 0;
+#pragma unroll
+          for (int cpy = 0; cpy < 8; ++cpy) v += hist[cpy][4 * lane + t];
+          cnt[t] = v;
+        }
+        const int sum4 = cnt[0] + cnt[1] + cnt[2] + cnt[3];
+        int suf = sum4;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_down(suf, o, 64);
+          if (lane + o < 64) suf += y;
+        }
+        int acc = suf - sum4;
+        for (int t = 3; t >= 0; --t) {
+          if (acc < krem && acc + cnt[t] >= krem) {
+            bcast[0] = 4 * lane + t;
+            bcast[1] = acc;
+            bcast[2] = cnt[t];
+          }
+          acc += cnt[t];
+        }
+      }
+      __syncthreads();
+      const uint32_t d = uint32_t(bcast[0]);
+      const int above = bcast[1], cntb = bcast[2];
+      __syncthreads();
+      const int sh = 24 - 8 * (j & 3);
+      if (j < 4) th |= d << sh; else if (j < 8) tl |= d << sh; else tp |= d << sh;
+      krem -= above;
+      fixed = j + 1;
+      if (cntb == krem) break;
+    }
+  }
+
+  // Phase 3a: kept-middle flags (unprotected and at or above the threshold prefix).
+  for (int w = threadIdx.x; w < (N + 31) / 32; w += SEL_THREADS) kbits[w] = 0;
+  __syncthreads();
+  if (k > 0) {
+    for (int c = threadIdx.x; c < N; c += SEL_THREADS) {
+      const uint32_t hi = keys[c];
+      if (hi == 0) continue;
+      bool kept = take_all;
+      if (!kept) {
+        const int ch = cmp96(hi, 0, 0, th, tl, tp, fixed < 4 ? fixed : 4);
+        if (ch != 0 || fixed <= 4) {
+          kept = ch >= 0;
+        } else {
+          const int32_t p = col_pos(a, lg, c);
+          const uint32_t lo = f64 ? uint32_t(col_key64(a, l, g, lg, c, p)) : 0u;
+          kept = cmp96(hi, lo, uint32_t(p), th, tl, tp, fixed) >= 0;
+        }
+      }
+      if (kept) atomicOr(&kbits[c >> 5], 1u << (c & 31));
+    }
+  }
+  __syncthreads();
+  if (P > a.budget) return;  // deferred: outputs untouched
+
+  // Phase 3b: kept middle columns ranked by position (bitmap over positions in the keys
+  // region, which is free now).
+  uint32_t* words = keys;
+  int* blockpre = reinterpret_cast<int*>(keys + a.nwords);
+  for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
+  __syncthreads();
+  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
+    int32_t pb[BATCH];
+    load_pos(k0, pb);
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = col(k0 + u);
+      if (c < N && (kbits[c >> 5] >> (c & 31) & 1u) && pb[u] < a.n) atomicOr(&words[pb[u] >> 5], 1u << (pb[u] & 31));
+    }
+  }
+  __syncthreads();
+  bitmap_prefix(words, a.nwords, blockpre, tmp);
+  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
+    int32_t pb[BATCH];
+    load_pos(k0, pb);
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = col(k0 + u);
+      if (c >= N || !(kbits[c >> 5] >> (c & 31) & 1u) || pb[u] >= a.n) continue;
+      const int r = bitmap_rank(words, blockpre, pb[u]);
+      if (r < k) {
+        a.middle[int64_t(lg) * a.budget + r] = c;
+        a.pos_new[int64_t(lg) * a.budget + P + r] = pb[u];
+      }
+    }
+  }
+  if (lg != 0) return;
+  // Head (0, 0): protected columns ranked by position.
+  __syncthreads();
+  for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
+  __syncthreads();
+  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
+    int32_t pb[BATCH];
+    load_pos(k0, pb);
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = col(k0 + u);
+      if (c < N && is_protected(a, pb[u]) && pb[u] < a.n) atomicOr(&words[pb[u] >> 5], 1u << (pb[u] & 31));
+    }
+  }
+  __syncthreads();
+  bitmap_prefix(words, a.nwords, blockpre, tmp);
+  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
+    int32_t pb[BATCH];
+    load_pos(k0, pb);
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = col(k0 + u);
+      if (c >= N || !is_protected(a, pb[u]) || pb[u] >= a.n) continue;
+      const int r = bitmap_rank(words, blockpre, pb[u]);
+      if (r < P) a.prot_cols[r] = c;
+    }
+  }
+}
+
 // --------------------------------------------------------- boundary kernels --
 
 struct BndArgs {
@@ -356,11 +658,28 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
   int* bc = tmp + 128;
   uint32_t* words = reinterpret_cast<uint32_t*>(bc + 16);
   const int LG = a.layers * a.kv_heads;
+  // Smallest and largest per-head protected count, reduced over the workgroup.
+  int mn = INT32_MAX, mx = INT32_MIN;
+  for (int i = threadIdx.x; i < LG; i += SEL_THREADS) {
+    const int v = a.prot_count[i];
+    mn = min(mn, v);
+    mx = max(mx, v);
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    mn = min(mn, __shfl_xor(mn, o, 64));
+    mx = max(mx, __shfl_xor(mx, o, 64));
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    tmp[wave] = mn;
+    tmp[64 + wave] = mx;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    int mn = a.prot_count[0], mx = a.prot_count[0];
-    for (int i = 1; i < LG; ++i) {
-      mn = min(mn, a.prot_count[i]);
-      mx = max(mx, a.prot_count[i]);
+    for (int w = 1; w < SEL_THREADS / 64; ++w) {
+      mn = min(mn, tmp[w]);
+      mx = max(mx, tmp[64 + w]);
     }
     const int P = a.prot_count[0];
     int state = GSE_BOUNDARY_EVICTED;
@@ -392,33 +711,47 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
     atomicOr(&words[c >> 5], 1u << (c & 31));
   }
   __syncthreads();
-  // Unprotected columns in column order: chunk of 32 columns per thread, scanned per pass.
+  int32_t* trow = a.table + int64_t(a.row) * a.table_stride;
+  // Unprotected columns in column order, 32 per thread per pass: target j = rank j < width
+  // (also the table's column P + j), leftover beyond.
   int carry = 0;
   for (int base = 0; base < a.nwords_cols; base += SEL_THREADS) {
     const int w = base + threadIdx.x;
-    const uint32_t free_bits = w < a.nwords_cols ? ~words[w] : 0u;
     const int64_t lo = int64_t(w) << 5;
-    uint32_t valid = 0;
-    if (w < a.nwords_cols) valid = lo + 32 <= a.N ? 0xffffffffu : ((1u << (a.N - lo)) - 1u);
-    const uint32_t bits = free_bits & valid;
+    uint32_t bits = 0;
+    if (w < a.nwords_cols) {
+      const uint32_t valid = lo + 32 <= a.N ? 0xffffffffu : ((1u << (a.N - lo)) - 1u);
+      bits = ~words[w] & valid;
+    }
     int total;
     const int ex = block_exclusive_scan<SEL_THREADS>(__popc(bits), tmp, &total);
     int j = carry + ex;
+    // The word's 32 slots are loaded together (slots has room for whole words), then stored.
+    int32_t sl[32];
+    if (bits) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int4 v = *reinterpret_cast<const int4*>(a.slots + lo + 4 * q);
+        sl[4 * q] = v.x;
+        sl[4 * q + 1] = v.y;
+        sl[4 * q + 2] = v.z;
+        sl[4 * q + 3] = v.w;
+      }
+    }
+#pragma unroll
     for (int t = 0; t < 32; ++t) {
       if (!(bits >> t & 1u)) continue;
-      const int32_t slot = a.slots[lo + t];
-      if (j < width)
-        a.targets[j] = slot;
-      else
-        a.leftover[j - width] = int64_t(slot);
+      if (j < width) {
+        a.targets[j] = sl[t];
+        trow[P + j] = sl[t];
+      } else {
+        a.leftover[j - width] = int64_t(sl[t]);
+      }
       ++j;
     }
     carry += total;
   }
-  __syncthreads();
-  int32_t* trow = a.table + int64_t(a.row) * a.table_stride;
   for (int i = threadIdx.x; i < P; i += SEL_THREADS) trow[i] = a.slots[a.prot_cols[i]];
-  for (int64_t j = threadIdx.x; j < width; j += SEL_THREADS) trow[P + j] = a.targets[j];
   if (threadIdx.x == 0) {
     a.count[a.row] = int32_t(P + width);
     a.frontier[a.row] = int32_t(a.n);
@@ -441,20 +774,89 @@ __global__ __launch_bounds__(256) void relocate_kernel(BndArgs a) {
   if (j >= width) return;
   const int32_t col = a.middle[int64_t(lg) * a.budget + j];
   const int64_t src = a.slots[col], dst = a.targets[j];
-  uint16_t* K = static_cast<uint16_t*>(a.k_pools[l]);
-  uint16_t* V = static_cast<uint16_t*>(a.v_pools[l]);
+  auto K = as_global(static_cast<uint16_t*>(a.k_pools[l]));
+  auto V = as_global(static_cast<uint16_t*>(a.v_pools[l]));
   const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
   uint16_t* sk = a.scratch_kv + ((int64_t(lg) * a.budget + j) * 2) * a.head_dim + 8 * piece;
   uint16_t* sv = sk + a.head_dim;
   float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
   if (DIR == 0) {
-    *reinterpret_cast<uint4*>(sk) = *reinterpret_cast<const uint4*>(K + src * a.kv_ss + off);
-    *reinterpret_cast<uint4*>(sv) = *reinterpret_cast<const uint4*>(V + src * a.kv_ss + off);
+    *reinterpret_cast<uint4*>(sk) = gload16(K + src * a.kv_ss + off);
+    *reinterpret_cast<uint4*>(sv) = gload16(V + src * a.kv_ss + off);
     if (piece == 0) a.scratch_sc[int64_t(lg) * a.budget + j] = srow[src * a.sss];
   } else {
-    *reinterpret_cast<uint4*>(K + dst * a.kv_ss + off) = *reinterpret_cast<const uint4*>(sk);
-    *reinterpret_cast<uint4*>(V + dst * a.kv_ss + off) = *reinterpret_cast<const uint4*>(sv);
+    gstore16(K + dst * a.kv_ss + off, *reinterpret_cast<const uint4*>(sk));
+    gstore16(V + dst * a.kv_ss + off, *reinterpret_cast<const uint4*>(sv));
     if (piece == 0) srow[dst * a.sss] = a.scratch_sc[int64_t(lg) * a.budget + j];
+  }
+}
+
+// Row-wise relocation for 8 KV heads x 64 dims (the pool row of a slot is 1 KiB): every
+// head's j-th kept middle column moves to the same target slot targets[j], so a wave moves
+// entry j of a layer at once: lane (head lane/8, piece lane%8) carries 16 bytes. The gather
+// (DIR 0) reads each head's 128-byte row from its own source slot and writes one contiguous
+// scratch row; the scatter (DIR 1) writes the target slot's whole K and V rows and its 8
+// scores. Grid (ceil(width / (4 * ROWS_PER_WAVE)), layers), 256 threads.
+constexpr int ROWS_PER_WAVE = 8;
+
+template <int DIR>
+__global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
+  const gse_boundary_status st = *a.status;
+  if (st.state != GSE_BOUNDARY_EVICTED || st.width <= 0) return;
+  const int64_t width = st.width;
+  const int l = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 3, piece = lane & 7;
+  const int lg = l * a.kv_heads + g;
+  auto K = as_global(static_cast<uint16_t*>(a.k_pools[l]));
+  auto V = as_global(static_cast<uint16_t*>(a.v_pools[l]));
+  const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
+  float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
+  const int64_t j0 = (int64_t(blockIdx.x) * 4 + wave) * ROWS_PER_WAVE;
+  // Scratch entry (l, j): K row (8 heads x 64) then V row, bf16; score row (8 heads).
+  auto sk = [&](int64_t j) { return a.scratch_kv + ((int64_t(l) * a.budget + j) * 2) * (8 * 64) + 64 * g + 8 * piece; };
+  auto ss = [&](int64_t j) { return a.scratch_sc + (int64_t(l) * a.budget + j) * 8 + g; };
+  if (DIR == 0) {
+    int64_t src[ROWS_PER_WAVE];
+#pragma unroll
+    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+      const int64_t j = j0 + r < width ? j0 + r : width - 1;
+      src[r] = a.slots[a.middle[int64_t(lg) * a.budget + j]];
+    }
+    uint4 kv[ROWS_PER_WAVE][2];
+    float sc[ROWS_PER_WAVE];
+#pragma unroll
+    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+      kv[r][0] = gload16(K + src[r] * a.kv_ss + off);
+      kv[r][1] = gload16(V + src[r] * a.kv_ss + off);
+      sc[r] = srow[src[r] * a.sss];
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+      if (j0 + r >= width) break;
+      *reinterpret_cast<uint4*>(sk(j0 + r)) = kv[r][0];
+      *reinterpret_cast<uint4*>(sk(j0 + r) + 8 * 64) = kv[r][1];
+      if (piece == 0) *ss(j0 + r) = sc[r];
+    }
+  } else {
+    int64_t dst[ROWS_PER_WAVE];
+    uint4 kv[ROWS_PER_WAVE][2];
+    float sc[ROWS_PER_WAVE];
+#pragma unroll
+    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+      const int64_t j = j0 + r < width ? j0 + r : width - 1;
+      dst[r] = a.targets[j];
+      kv[r][0] = *reinterpret_cast<const uint4*>(sk(j));
+      kv[r][1] = *reinterpret_cast<const uint4*>(sk(j) + 8 * 64);
+      sc[r] = *ss(j);
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+      if (j0 + r >= width) break;
+      gstore16(K + dst[r] * a.kv_ss + off, kv[r][0]);
+      gstore16(V + dst[r] * a.kv_ss + off, kv[r][1]);
+      if (piece == 0) srow[dst[r] * a.sss] = sc[r];
+    }
   }
 }
 
@@ -512,47 +914,50 @@ GSE_DEVICE uint32_t bitmap_load(const uint32_t* p) { return __hip_atomic_load(p,
 GSE_DEVICE void bitmap_clear(uint32_t* p) { __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 // Single workgroup: pack the owned slots that are not real at the start of the row (R:485-491).
+// The membership bitmap of the real slots is in LDS when the pool fits (LDS_BITMAP), else in
+// the caller's workspace.
+constexpr int64_t REPACK_LDS_WORDS = 36864;
+
+template <bool LDS_BITMAP>
 __global__ __launch_bounds__(SEL_THREADS) void repack_kernel(LiveArgs a) {
   __shared__ int tmp[128 + 16];
+  __shared__ uint32_t lbits[LDS_BITMAP ? REPACK_LDS_WORDS : 1];
   if (a.status->state != GSE_BOUNDARY_EVICTED) return;
   const int64_t cnt = a.status->count;
   const int64_t nw = (a.num_slots + 31) >> 5;
-  for (int64_t i = threadIdx.x; i < nw; i += SEL_THREADS) bitmap_clear(&a.bitmap[i]);
+  uint32_t* bits = LDS_BITMAP ? lbits : a.bitmap;
+  for (int64_t i = threadIdx.x; i < nw; i += SEL_THREADS) {
+    if constexpr (LDS_BITMAP) lbits[i] = 0; else bitmap_clear(&a.bitmap[i]);
+  }
   __syncthreads();
   int32_t* rrow = a.r2t + int64_t(a.row) * a.r2t_stride;
   for (int64_t p = a.true_len + threadIdx.x; p < a.n; p += SEL_THREADS) {
     const int64_t s = rrow[p];
-    if (s >= 0 && s < a.num_slots) atomicOr(&a.bitmap[s >> 5], 1u << (s & 31));
+    if (s >= 0 && s < a.num_slots) atomicOr(&bits[s >> 5], 1u << (s & 31));
   }
   __syncthreads();
+  auto is_real = [&](int64_t s) -> bool {
+    if constexpr (LDS_BITMAP) return lbits[s >> 5] >> (s & 31) & 1u;
+    else return bitmap_load(&a.bitmap[s >> 5]) >> (s & 31) & 1u;
+  };
   const int32_t* trow = a.table + int64_t(a.row) * a.table_stride;
-  // Count packed entries first; only write if they fit below true_len.
-  int mine = 0;
-  for (int64_t i = threadIdx.x; i < cnt; i += SEL_THREADS) {
-    const int64_t s = trow[i];
-    mine += !(bitmap_load(&a.bitmap[s >> 5]) >> (s & 31) & 1u);
-  }
-  const int packed = block_sum(mine, tmp);
+  // In-order compaction: contiguous ranges per thread keep the table order.
+  const int64_t per = (cnt + SEL_THREADS - 1) / SEL_THREADS;
+  const int64_t lo = threadIdx.x * per, hi = min(cnt, lo + per);
+  int c = 0;
+  for (int64_t i = lo; i < hi; ++i) c += !is_real(trow[i]);
+  int packed;
+  int j = block_exclusive_scan<SEL_THREADS>(c, tmp, &packed);
   if (threadIdx.x == 0) a.status->packed = packed;
   if (packed > a.true_len) {
     if (threadIdx.x == 0) a.status->state = GSE_BOUNDARY_ERR_PACKED;
     return;
   }
-  // In-order compaction: contiguous ranges per thread keep the table order.
-  const int64_t per = (cnt + SEL_THREADS - 1) / SEL_THREADS;
-  const int64_t lo = threadIdx.x * per, hi = min(cnt, lo + per);
-  int c = 0;
-  for (int64_t i = lo; i < hi; ++i) {
-    const int64_t s = trow[i];
-    c += !(bitmap_load(&a.bitmap[s >> 5]) >> (s & 31) & 1u);
-  }
-  int total;
-  int j = block_exclusive_scan<SEL_THREADS>(c, tmp, &total);
   // Rows [packed, true_len) become holes; [0, packed) get the packed slots.
   for (int64_t i = packed + threadIdx.x; i < a.true_len; i += SEL_THREADS) rrow[i] = 0;
   for (int64_t i = lo; i < hi; ++i) {
     const int64_t s = trow[i];
-    if (!(bitmap_load(&a.bitmap[s >> 5]) >> (s & 31) & 1u)) rrow[j++] = int32_t(s);
+    if (!is_real(s)) rrow[j++] = int32_t(s);
   }
 }
 
@@ -586,7 +991,7 @@ BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t 
   const int64_t LG = int64_t(layers) * kv_heads;
   BndLayout L;
   int64_t o = 0;
-  L.slots = o; o += align256(N * 4);
+  L.slots = o; o += align256(((N + 31) / 32) * 32 * 4);  // whole 32-column words
   L.keys = o; o += align256(LG * N * 8);
   L.posw = o; o += align256(LG * N * 4);
   L.prot = o; o += align256(LG * 4);
@@ -762,19 +1167,32 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   a.prot_cols = b.prot_cols;
   a.pos_new = pos_new;
   a.nwords = int((n + 31) / 32);
-  hipLaunchKernelGGL(select_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), select_lds_bytes(a.nwords), s, a);
+  // The position bitmap (and its prefix counts) must fit in the LDS key array of the fast path.
+  const int64_t bitmap_words = a.nwords + (a.nwords + 31) / 32;
+  if (N <= SEL_LDS_KEYS && bitmap_words <= SEL_LDS_KEYS)
+    hipLaunchKernelGGL(select_row_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), 0, s, a);
+  else
+    hipLaunchKernelGGL(select_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), select_lds_bytes(a.nwords), s, a);
   if (int rc = gse_launch_check("boundary select")) return rc;
 
   const size_t col_lds = size_t(128 + 16) * 4 + size_t(b.nwords_cols) * 4 + 16;
   hipLaunchKernelGGL(columns_kernel, dim3(1), dim3(SEL_THREADS), col_lds, s, b);
   if (int rc = gse_launch_check("boundary columns")) return rc;
 
-  const int chunks = head_dim / 8;
-  const dim3 rgrid(unsigned((budget * chunks + 255) / 256), unsigned(LG));
-  hipLaunchKernelGGL(relocate_kernel<0>, rgrid, dim3(256), 0, s, b);
-  if (int rc = gse_launch_check("boundary gather")) return rc;
-  hipLaunchKernelGGL(relocate_kernel<1>, rgrid, dim3(256), 0, s, b);
-  if (int rc = gse_launch_check("boundary scatter")) return rc;
+  if (kv_heads == 8 && head_dim == 64) {
+    const dim3 rgrid(unsigned((budget + 4 * ROWS_PER_WAVE - 1) / (4 * ROWS_PER_WAVE)), unsigned(layers));
+    hipLaunchKernelGGL(relocate_rows_kernel<0>, rgrid, dim3(256), 0, s, b);
+    if (int rc = gse_launch_check("boundary gather")) return rc;
+    hipLaunchKernelGGL(relocate_rows_kernel<1>, rgrid, dim3(256), 0, s, b);
+    if (int rc = gse_launch_check("boundary scatter")) return rc;
+  } else {
+    const int chunks = head_dim / 8;
+    const dim3 rgrid(unsigned((budget * chunks + 255) / 256), unsigned(LG));
+    hipLaunchKernelGGL(relocate_kernel<0>, rgrid, dim3(256), 0, s, b);
+    if (int rc = gse_launch_check("boundary gather")) return rc;
+    hipLaunchKernelGGL(relocate_kernel<1>, rgrid, dim3(256), 0, s, b);
+    if (int rc = gse_launch_check("boundary scatter")) return rc;
+  }
   hipLaunchKernelGGL(protected_pos_kernel, dim3(unsigned(LG)), dim3(256), 0, s, b);
   return gse_launch_check("boundary protected pos");
 }
@@ -802,6 +1220,9 @@ extern "C" int gse_boundary_live(float* scores, int layers, int64_t scores_strid
   }
   hipLaunchKernelGGL(zero_leftover_kernel, dim3(256), dim3(256), 0, s, a);
   if (int rc = gse_launch_check("zero leftover")) return rc;
-  hipLaunchKernelGGL(repack_kernel, dim3(1), dim3(SEL_THREADS), 0, s, a);
+  if ((num_slots + 31) / 32 <= REPACK_LDS_WORDS)
+    hipLaunchKernelGGL(repack_kernel<true>, dim3(1), dim3(SEL_THREADS), 0, s, a);
+  else
+    hipLaunchKernelGGL(repack_kernel<false>, dim3(1), dim3(SEL_THREADS), 0, s, a);
   return gse_launch_check("repack");
 }

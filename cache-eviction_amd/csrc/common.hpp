@@ -56,6 +56,24 @@ GSE_DEVICE bf16x8_t join_bf16x8(s16x4_t lo, s16x4_t hi) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// A pointer read from device memory (e.g. a per-layer pool table) is a generic pointer to the
+// compiler; naming its global address space lets it issue global (not flat) loads and stores,
+// whose waits it tracks per access.
+template <typename T>
+GSE_DEVICE __attribute__((address_space(1))) T* as_global(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+
+// 16-byte global load / store through an address-space-1 pointer.
+GSE_DEVICE uint4 gload16(const __attribute__((address_space(1))) void* p) {
+  return __builtin_bit_cast(uint4, *(const __attribute__((address_space(1))) u32x4_t*)p);
+}
+GSE_DEVICE void gstore16(__attribute__((address_space(1))) void* p, uint4 v) {
+  *(__attribute__((address_space(1))) u32x4_t*)p = __builtin_bit_cast(u32x4_t, v);
+}
+
 template <typename T>
 GSE_DEVICE int64_t load_index(const void* p, int64_t i) {
   return int64_t(static_cast<const T*>(p)[i]);

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void score_flush_kernel(FlushArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
   const int64_t cnt = a.count[row], fr = a.frontier[row];
-  const uint16_t* kp = static_cast<const uint16_t*>(a.k_pools[l]) + int64_t(g) * a.kv_sh + 8 * grp;
+  const auto kp = as_global(static_cast<const uint16_t*>(a.k_pools[l])) + int64_t(g) * a.kv_sh + 8 * grp;
   float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
   const int npairs = (m + 1) >> 1;
 
@@ -124,9 +124,9 @@ __global__ __launch_bounds__(256) void score_flush_kernel(FlushArgs a) {
       const int cc = c < maxlim ? c : maxlim - 1;
       const int32_t s = cc < cnt ? a.table[row * a.table_stride + cc] : a.r2t[row * a.r2t_stride + fr + cc - cnt];
       slot[st] = c < maxlim ? s : 0;
-      const uint16_t* p = kp + uint64_t(uint32_t(slot[st])) * uint64_t(a.kv_ss);
-      kf[st][0] = *reinterpret_cast<const uint4*>(p);
-      kf[st][1] = *reinterpret_cast<const uint4*>(p + 32);
+      const auto p = kp + uint64_t(uint32_t(slot[st])) * uint64_t(a.kv_ss);
+      kf[st][0] = gload16(p);
+      kf[st][1] = gload16(p + 32);
     }
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int pr = 0; pr < npairs; ++pr) {
