@@ -60,8 +60,11 @@ GSE_DEVICE bf16x8_t join_bf16x8(s16x4_t lo, s16x4_t hi) {
 // compiler; naming its global address space lets it issue global (not flat) loads and stores,
 // whose waits it tracks per access.
 template <typename T>
-GSE_DEVICE __attribute__((address_space(1))) T* as_global(T* p) {
-  return (__attribute__((address_space(1))) T*)p;
+using global_ptr = __attribute__((address_space(1))) T*;
+
+template <typename T>
+GSE_DEVICE global_ptr<T> as_global(T* p) {
+  return (global_ptr<T>)p;
 }
 
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;

@@ -25,9 +25,10 @@ namespace gse {
 namespace fl {
 constexpr int D = 64;
 constexpr int GROUP = 8;
-constexpr int WAVES = 4;
+constexpr int WAVES = 8;
+constexpr int THREADS = WAVES * 64;
 constexpr int TILE = 64;
-constexpr int TILES_PER_WAVE = 4;
+constexpr int TILES_PER_WAVE = 2;
 constexpr int CHUNK = WAVES * TILES_PER_WAVE * TILE;  // keys per workgroup
 constexpr int MAX_QUEUE = 64;
 constexpr int QROW = D + 8;  // padded bf16 row of a queued (query, head) in LDS
@@ -58,12 +59,90 @@ struct FlushArgs {
   float scale2;  // sm_scale * log2(e)
 };
 
-// Grid (key chunks, n_rows, layers * kv_heads), 256 threads.
-__global__ __launch_bounds__(256) void score_flush_kernel(FlushArgs a) {
+// One 64-key tile of a wave: K of keys tb + 16*st + col in registers, then per pair of
+// queued queries eight MFMAs (four 16-key sub-tiles) and the exponentials. Sum mode adds
+// each lane's four heads in-lane and leaves the head/query reduction across lanes to the
+// end; max mode needs the per-query maximum over eight heads, one lane swap per pair.
+// Pairs whose shorter list covers the whole tile skip the causal mask; pairs whose longer
+// list ends before the tile are skipped.
+// Adds one pair's exponentials of sub-tile st (keys tb + 16*st + col) to acc.
+template <bool MAX_MODE, bool MASKED>
+GSE_DEVICE float flush_add(f32x4_t d, f32x4_t nrm, float scale2, bool live, float acc) {
+  const float e0 = fast_exp2(fmaf(d[0], scale2, -nrm[0]));
+  const float e1 = fast_exp2(fmaf(d[1], scale2, -nrm[1]));
+  const float e2 = fast_exp2(fmaf(d[2], scale2, -nrm[2]));
+  const float e3 = fast_exp2(fmaf(d[3], scale2, -nrm[3]));
+  if (MAX_MODE) {
+    const float red = fmaxf(fmaxf(e0, e1), fmaxf(e2, e3));
+    return acc + xor16_max(!MASKED || live ? red : 0.f);
+  }
+  const float red = (e0 + e1) + (e2 + e3);
+  return acc + (!MASKED || live ? red : 0.f);
+}
+
+template <bool MAX_MODE>
+GSE_DEVICE void flush_tile(const FlushArgs& a, const uint16_t* qs, const float* ns, const int* lims,
+                           const int* pmin, const int* pmax, int npairs, int tb, int maxlim, int64_t row, int64_t cnt,
+                           int64_t fr, global_ptr<const uint16_t> kp, float* srow) {
+  using namespace fl;
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  int32_t slot[4];
+  uint4 kf[4][2];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const int c = tb + 16 * st + col;
+    const int cc = c < maxlim ? c : maxlim - 1;
+    const int32_t s = cc < cnt ? a.table[row * a.table_stride + cc] : a.r2t[row * a.r2t_stride + fr + cc - cnt];
+    slot[st] = c < maxlim ? s : 0;
+    const auto p = kp + uint64_t(uint32_t(slot[st])) * uint64_t(a.kv_ss);
+    kf[st][0] = gload16(p);
+    kf[st][1] = gload16(p + 32);
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int pr = 0; pr < npairs; ++pr) {
+    if (__builtin_amdgcn_readfirstlane(pmax[pr]) <= tb) continue;  // both lists end before this tile
+    const bool masked = __builtin_amdgcn_readfirstlane(pmin[pr]) < tb + TILE;
+    // A rows: (query 2*pr + col/8, head col%8); this lane's D rows: query 2*pr + grp/2,
+    // heads 4*(grp%2) + r.
+    const uint16_t* qrow = qs + ((2 * pr) * GROUP + col) * QROW + 8 * grp;
+    const bf16x8_t qa0 = as_bf16x8(*reinterpret_cast<const uint4*>(qrow));
+    const bf16x8_t qa1 = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + 32));
+    const int qi = 2 * pr + (grp >> 1);
+    const f32x4_t nrm = *reinterpret_cast<const f32x4_t*>(ns + qi * GROUP + 4 * (grp & 1));
+    f32x4_t d[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      d[st] = mfma16x16x32(qa0, as_bf16x8(kf[st][0]), f32x4_t{0.f, 0.f, 0.f, 0.f});
+      d[st] = mfma16x16x32(qa1, as_bf16x8(kf[st][1]), d[st]);
+    }
+    if (masked) {
+      const int lim = lims[qi];
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        acc[st] = flush_add<MAX_MODE, true>(d[st], nrm, a.scale2, tb + 16 * st + col < lim, acc[st]);
+    } else {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) acc[st] = flush_add<MAX_MODE, false>(d[st], nrm, a.scale2, true, acc[st]);
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    // Sum mode: lanes of all four groups hold partial sums. Max mode: groups 0/1 hold the
+    // even queries' sums (twice), 2/3 the odd ones'.
+    const float tot = MAX_MODE ? xor32_sum(acc[st]) : xor32_sum(xor16_sum(acc[st]));
+    const int c = tb + 16 * st + col;
+    if (grp == 0 && c < maxlim) unsafeAtomicAdd(srow + uint64_t(uint32_t(slot[st])) * a.sss, tot);
+  }
+}
+
+// Grid (key chunks, n_rows, layers * kv_heads), THREADS threads.
+__global__ __launch_bounds__(fl::THREADS) void score_flush_kernel(FlushArgs a) {
   using namespace fl;
   __shared__ __attribute__((aligned(16))) uint16_t qs[MAX_QUEUE * GROUP * QROW];
   __shared__ __attribute__((aligned(16))) float ns[MAX_QUEUE * GROUP];
   __shared__ int lims[MAX_QUEUE];
+  __shared__ int pmin[MAX_QUEUE / 2], pmax[MAX_QUEUE / 2];
 
   const int lg = blockIdx.z;
   const int l = lg / a.kv_heads, g = lg % a.kv_heads;
@@ -74,7 +153,6 @@ __global__ __launch_bounds__(256) void score_flush_kernel(FlushArgs a) {
   int m = a.pcount[qbase];
   m = m < a.cap ? m : a.cap;
   if (m <= 0) return;
-  const bool max_mode = md == 2;
 
   // Queued lengths: the workgroup's keys are [c0, min(c0 + CHUNK, max lim)).
   if (threadIdx.x < m) lims[threadIdx.x] = a.plim[qbase * a.cap + threadIdx.x];
@@ -96,74 +174,38 @@ __global__ __launch_bounds__(256) void score_flush_kernel(FlushArgs a) {
     const int qi = t / GROUP, h = t % GROUP;
     ns[t] = a.pnorm[(qbase * a.cap + qi) * a.q_heads + g * GROUP + h] * kLog2e;
   }
-  // Odd queue lengths: the missing query of the last pair carries no mass.
+  // Odd queue lengths: the missing query of the last pair carries no mass (its normaliser
+  // is +inf, so every exponential is 0) and is never masked.
   if (m & 1) {
     for (int t = threadIdx.x; t < GROUP; t += blockDim.x) ns[m * GROUP + t] = INFINITY;
     for (int t = threadIdx.x; t < GROUP * (D / 8); t += blockDim.x)
       *reinterpret_cast<uint4*>(qs + (m * GROUP + t / (D / 8)) * QROW + 8 * (t % (D / 8))) = uint4{0, 0, 0, 0};
-    if (threadIdx.x == 0) lims[m] = 0;
+  }
+  const int npairs = (m + 1) >> 1;
+  if (threadIdx.x < npairs) {
+    const int l0 = lims[2 * threadIdx.x];
+    const int l1 = 2 * threadIdx.x + 1 < m ? lims[2 * threadIdx.x + 1] : l0;
+    pmin[threadIdx.x] = l0 < l1 ? l0 : l1;
+    pmax[threadIdx.x] = l0 < l1 ? l1 : l0;
   }
   __syncthreads();
+  if (m & 1) {
+    if (threadIdx.x == 0) lims[m] = lims[m - 1];
+    __syncthreads();
+  }
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int col = lane & 15, grp = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform tile bases
   const int64_t cnt = a.count[row], fr = a.frontier[row];
-  const auto kp = as_global(static_cast<const uint16_t*>(a.k_pools[l])) + int64_t(g) * a.kv_sh + 8 * grp;
+  const auto kp =
+      as_global(static_cast<const uint16_t*>(a.k_pools[l])) + int64_t(g) * a.kv_sh + 8 * ((threadIdx.x & 63) >> 4);
   float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
-  const int npairs = (m + 1) >> 1;
-
   for (int ti = 0; ti < TILES_PER_WAVE; ++ti) {
     const int tb = c0 + (ti * WAVES + wave) * TILE;
     if (tb >= maxlim) break;
-    // Slots and K fragments of keys tb + 16*st + col (lanes past the list read slot 0).
-    int32_t slot[4];
-    uint4 kf[4][2];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const int c = tb + 16 * st + col;
-      const int cc = c < maxlim ? c : maxlim - 1;
-      const int32_t s = cc < cnt ? a.table[row * a.table_stride + cc] : a.r2t[row * a.r2t_stride + fr + cc - cnt];
-      slot[st] = c < maxlim ? s : 0;
-      const auto p = kp + uint64_t(uint32_t(slot[st])) * uint64_t(a.kv_ss);
-      kf[st][0] = gload16(p);
-      kf[st][1] = gload16(p + 32);
-    }
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int pr = 0; pr < npairs; ++pr) {
-      // A rows: (query 2*pr + col/8, head col%8); this lane's D rows: query 2*pr + grp/2,
-      // heads 4*(grp%2) + r.
-      const uint16_t* qrow = qs + ((2 * pr) * GROUP + col) * QROW + 8 * grp;
-      const bf16x8_t qa0 = as_bf16x8(*reinterpret_cast<const uint4*>(qrow));
-      const bf16x8_t qa1 = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + 32));
-      const int qi = 2 * pr + (grp >> 1);
-      const f32x4_t nrm = *reinterpret_cast<const f32x4_t*>(ns + qi * GROUP + 4 * (grp & 1));
-      const int lim = lims[qi];
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        f32x4_t d = {0.f, 0.f, 0.f, 0.f};
-        d = mfma16x16x32(qa0, as_bf16x8(kf[st][0]), d);
-        d = mfma16x16x32(qa1, as_bf16x8(kf[st][1]), d);
-        const bool live = tb + 16 * st + col < lim;
-        float red;
-        if (max_mode) {
-          red = fmaxf(fmaxf(fast_exp2(fmaf(d[0], a.scale2, -nrm[0])), fast_exp2(fmaf(d[1], a.scale2, -nrm[1]))),
-                      fmaxf(fast_exp2(fmaf(d[2], a.scale2, -nrm[2])), fast_exp2(fmaf(d[3], a.scale2, -nrm[3]))));
-          red = xor16_max(live ? red : 0.f);
-        } else {
-          red = (fast_exp2(fmaf(d[0], a.scale2, -nrm[0])) + fast_exp2(fmaf(d[1], a.scale2, -nrm[1]))) +
-                (fast_exp2(fmaf(d[2], a.scale2, -nrm[2])) + fast_exp2(fmaf(d[3], a.scale2, -nrm[3])));
-          red = xor16_sum(live ? red : 0.f);
-        }
-        acc[st] += red;
-      }
-    }
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      // Lanes of groups 0/1 hold even queries' sums, 2/3 odd ones'.
-      const float tot = xor32_sum(acc[st]);
-      const int c = tb + 16 * st + col;
-      if (grp == 0 && c < maxlim) unsafeAtomicAdd(srow + uint64_t(uint32_t(slot[st])) * a.sss, tot);
-    }
+    if (md == 2)
+      flush_tile<true>(a, qs, ns, lims, pmin, pmax, npairs, tb, maxlim, row, cnt, fr, kp, srow);
+    else
+      flush_tile<false>(a, qs, ns, lims, pmin, pmax, npairs, tb, maxlim, row, cnt, fr, kp, srow);
   }
 }
 
@@ -210,8 +252,8 @@ extern "C" int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stri
                  layers, q_heads, kv_heads, sm_scale * kLog2e};
   const unsigned chunks = unsigned((max_len + CHUNK - 1) / CHUNK);
   if (chunks) {
-    hipLaunchKernelGGL(score_flush_kernel, dim3(chunks, unsigned(n_rows), unsigned(layers * kv_heads)), dim3(256), 0,
-                       s, f);
+    hipLaunchKernelGGL(score_flush_kernel, dim3(chunks, unsigned(n_rows), unsigned(layers * kv_heads)), dim3(THREADS),
+                       0, s, f);
     if (int rc = gse_launch_check("score_flush")) return rc;
   }
   const int total = n_rows * layers;
