@@ -185,7 +185,9 @@ class Workload:
             st.frontier[row] = f
         st.req_to_token.copy_(r2t.to(dev))
         st.table.copy_(table.to(dev))
-        self.new_slots = torch.stack(self.new_slots).to(dev)  # [bs, steps]
+        # Each step's new slots, contiguous: int64 for out_cache_loc, int32 for req_to_token.
+        self.new_slots = torch.stack(self.new_slots).t().contiguous().to(dev)  # [steps, bs]
+        self.new_slots32 = self.new_slots.int()
         self.rows = torch.arange(1, bs + 1, device=dev)
         self.rows_host = list(range(1, bs + 1))
         self.lens = list(lens)
@@ -222,10 +224,9 @@ class Workload:
                     self.boundaries += 1
         # Allocate the new token's slot (SGLang's allocator), then the CSR for every full layer.
         t = self.step_index
-        new = self.new_slots[:, t]
-        lens_t = self.seq_lens
-        st.req_to_token[self.rows, lens_t] = new.int()
-        self.seq_lens = lens_t + 1
+        new = self.new_slots[t]
+        st.req_to_token[self.rows, self.seq_lens] = self.new_slots32[t]
+        self.seq_lens.add_(1)
         self.lens = [n + 1 for n in self.lens]
         bs = a.bs
         ge.begin_decode_step(self.rows_host, st)  # flushes rows whose score queue is full
@@ -252,7 +253,7 @@ def kernel_roofline(w, reps):
     inputs, with HIP events on the launch stream, and its algorithmic bytes per launch."""
     torch, ge, a = w.torch, w.ge, w.args
     bs = a.bs
-    fb = SimpleNamespace(out_cache_loc=w.new_slots[:, max(w.step_index - 1, 0)], req_pool_indices=w.rows,
+    fb = SimpleNamespace(out_cache_loc=w.new_slots[max(w.step_index - 1, 0)], req_pool_indices=w.rows,
                          seq_lens_cpu=w.max_resident_list())
     # Resident counts of the last step (the CSR already in kv_indices).
     res = [w.resident(i) for i in range(bs)]

@@ -281,13 +281,20 @@ struct MergeArgs {
   int bs, q_heads, nparts;  // nparts = P, the fused kernel's workgroup count
 };
 
-// Grid (bs): thread (head t/8, dims [8*(t%8), +8)) merges the partials of its head with
-// the sink: o = sum_w 2^(m_w - M) o_w / (2^(sink - M) + sum_w 2^(m_w - M) l_w), M the maximum.
-__global__ __launch_bounds__(512) void decode_merge_kernel(MergeArgs a) {
+// Grid (bs), MERGE_THREADS threads: thread (head t/16, dims [4*(t%16), +4)) merges the
+// partials of its head with the sink:
+//   o = sum_w 2^(m_w - M) o_w / (2^(sink - M) + sum_w 2^(m_w - M) l_w), M the maximum,
+// MERGE_BATCH partials at a time with all their loads in flight together (a partial past
+// the range is read again with weight 0), one rescale of the running sums per batch.
+constexpr int MERGE_THREADS = 1024;
+constexpr int MERGE_BATCH = 8;
+
+__global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(MergeArgs a) {
   const int b = blockIdx.x;
-  const int h = threadIdx.x >> 3;
-  const int j = threadIdx.x & 7;
-  // Every thread reads the queue slot before thread 0 advances it.
+  const int h = threadIdx.x >> 4;
+  const int j = threadIdx.x & 15;
+  // Independent loads first: the queue slot (row -> mode, count) and the partial range
+  // (indptr) are two short chains issued together.
   int64_t row = 0;
   int slot = 0;
   bool queue = false;
@@ -297,8 +304,9 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(MergeArgs a) {
     slot = a.qcount[row];
     queue = md == 1 || md == 2;
   }
-  __syncthreads();
-  if (h >= a.q_heads) return;
+  const bool live = h < a.q_heads;
+  const int hh = live ? h : 0;
+  const uint2 qv = *reinterpret_cast<const uint2*>(a.q + int64_t(b) * a.q_sb + int64_t(hh) * a.q_sh + 4 * j);
   const int T = a.indptr[a.bs];
   const int C = fused_chunk(T, a.nparts);
   const int start = a.indptr[b], end = a.indptr[b + 1];
@@ -307,47 +315,48 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(MergeArgs a) {
     wf = start / C;
     wl = (end - 1) / C;
   }
-  // Online merge from the sink's state (m = sink, l = 1, o = 0), four partials per batch with
-  // their loads issued together (a partial past the range is read again with weight 0).
-  float mx = load_float_dyn(a.sinks, a.sinks_dtype, h) * kLog2e;
+  float mx = load_float_dyn(a.sinks, a.sinks_dtype, hh) * kLog2e;
   float lsum = 1.f;
-  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  for (int w0 = wf; w0 <= wl; w0 += 4) {
-    float pm[4], pl[4];
-    f32x4_t po0[4], po1[4];
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int w0 = wf; w0 <= wl; w0 += MERGE_BATCH) {
+    float pm[MERGE_BATCH], pl[MERGE_BATCH];
+    f32x4_t po[MERGE_BATCH];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < MERGE_BATCH; ++k) {
       const int w = w0 + k <= wl ? w0 + k : wl;
-      const float* ps = a.part + ((int64_t(w) + b) * a.q_heads + h) * PART;
+      const float* ps = a.part + ((int64_t(w) + b) * a.q_heads + hh) * PART;
       pm[k] = w0 + k <= wl ? ps[D] : -INFINITY;
       pl[k] = ps[D + 1];
-      po0[k] = *reinterpret_cast<const f32x4_t*>(ps + 8 * j);
-      po1[k] = *reinterpret_cast<const f32x4_t*>(ps + 8 * j + 4);
+      po[k] = *reinterpret_cast<const f32x4_t*>(ps + 4 * j);
     }
+    float m_new = mx;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float m_new = fmaxf(mx, pm[k]);
-      const float so = fast_exp2(mx - m_new), sk = fast_exp2(pm[k] - m_new);
-      lsum = lsum * so + pl[k] * sk;
-      acc0 = acc0 * so + po0[k] * sk;
-      acc1 = acc1 * so + po1[k] * sk;
-      mx = m_new;
+    for (int k = 0; k < MERGE_BATCH; ++k) m_new = fmaxf(m_new, pm[k]);
+    const float so = fast_exp2(mx - m_new);
+    lsum *= so;
+    acc = acc * so;
+#pragma unroll
+    for (int k = 0; k < MERGE_BATCH; ++k) {
+      const float sk = fast_exp2(pm[k] - m_new);
+      lsum += pl[k] * sk;
+      acc += po[k] * sk;
     }
+    mx = m_new;
   }
+  // Every thread has read the queue slot before thread 0 advances it.
+  __syncthreads();
+  if (queue && threadIdx.x == 0) a.qcount[row] = slot + 1;
+  if (!live) return;
   const float inv = 1.f / lsum;
-  uint4 out;
-  out.x = pack_bf16x2(acc0[0] * inv, acc0[1] * inv);
-  out.y = pack_bf16x2(acc0[2] * inv, acc0[3] * inv);
-  out.z = pack_bf16x2(acc1[0] * inv, acc1[1] * inv);
-  out.w = pack_bf16x2(acc1[2] * inv, acc1[3] * inv);
-  *reinterpret_cast<uint4*>(a.o + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + 8 * j) = out;
+  uint2 out;
+  out.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+  out.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<uint2*>(a.o + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + 4 * j) = out;
   const float norm = (mx + __log2f(lsum)) * kLn2;
   if (j == 0) a.norm_out[int64_t(b) * a.q_heads + h] = norm;
-  if (queue && threadIdx.x == 0) a.qcount[row] = slot + 1;
   if (queue && slot < a.cap) {
     const int64_t e = row * a.cap + slot;
-    *reinterpret_cast<uint4*>(a.qq + (e * a.q_heads + h) * D + 8 * j) =
-        *reinterpret_cast<const uint4*>(a.q + int64_t(b) * a.q_sb + int64_t(h) * a.q_sh + 8 * j);
+    *reinterpret_cast<uint2*>(a.qq + (e * a.q_heads + h) * D + 4 * j) = qv;
     if (j == 0) a.qnorm[e * a.q_heads + h] = norm;
     if (threadIdx.x == 0) a.qlim[e] = end - start;
   }
@@ -595,7 +604,7 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   m.bs = bs;
   m.q_heads = q_heads;
   m.nparts = P;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(bs), dim3(512), 0, s, m);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(bs), dim3(MERGE_THREADS), 0, s, m);
   if ((rc = gse_launch_check("decode_merge"))) return rc;
 
   if (score_mode == GSE_SCORE_EAGER) {
