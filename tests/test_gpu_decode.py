@@ -97,18 +97,18 @@ def _oracle_step(b, st, q, sinks, perm, indptr, lid, mode):
 
 
 @pytest.mark.parametrize("mode", [1, 2])
-@pytest.mark.parametrize("lag", [False, True])
-def test_fused_decode_matches_oracle(mode, lag):
+@pytest.mark.parametrize("queued", [False, True])
+def test_fused_decode_matches_oracle(mode, queued):
     lengths = [37, 1500, 3001]
     b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths)
-    st.score_mode = "queue" if lag else "eager"
+    st.score_mode = "queue" if queued else "eager"
     st.mode[:] = mode
     b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=perm)
     fb = SimpleNamespace(out_cache_loc=torch.zeros(3, dtype=torch.int64, device="cuda"), req_pool_indices=rows,
                          seq_lens_cpu=torch.tensor(lengths))
     o = torch.empty_like(q)
     assert ge.decode(b, q.reshape(3, -1), layer(1), fb, sinks, o.reshape(3, -1))
-    if lag:
+    if queued:
         assert float(st.scores.abs().sum()) == 0.0  # the step is queued until flushed
         # The flush rebuilds each row's list from the eviction state (empty table, tail = req_to_token).
         for i, r in enumerate(rows.tolist()):
@@ -128,11 +128,11 @@ def test_queue_over_steps_equals_eager():
     """Several decode steps with growing lists: queued + flushed scores equal eager ones."""
     g = torch.Generator().manual_seed(3)
     results = {}
-    for lag in (False, True):
+    for queued in (False, True):
         ge.STATE = None
         b = backend(gen=torch.Generator().manual_seed(1))
         st = ge.state(b)
-        st.score_mode = "queue" if lag else "eager"
+        st.score_mode = "queue" if queued else "eager"
         st.mode[:] = 1
         base = [100, 700]
         perm = (torch.randperm(19999, generator=torch.Generator().manual_seed(2))[:2000] + 1).cuda()
@@ -152,7 +152,7 @@ def test_queue_over_steps_equals_eager():
         st.req_to_token[1, :base[0] + 3] = perm[:base[0] + 3].int()
         st.req_to_token[2, :base[1] + 3] = perm[1000:1000 + base[1] + 3].int()
         ge.flush(st)
-        results[lag] = st.scores.clone()
+        results[queued] = st.scores.clone()
     # Only the fp32 summation order differs (per step vs per queue).
     torch.testing.assert_close(results[True], results[False], rtol=1e-5, atol=1e-8)
 
