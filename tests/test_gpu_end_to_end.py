@@ -1,0 +1,169 @@
+"""The reference's CPU-runnable case end to end, through the hooks SGLang calls.
+
+One full-attention layer (64 query heads, 8 KV heads, d=64), Q/K/V ~ N(0, 1) from seed 0,
+scale 1/sqrt(64), sink logits ~ N(0, 1). A 4096-token prompt arrives in two 2048-token
+chunks (`on_extend` + `after_extend`), then decode steps run `on_decode`, `fill` and the
+fused `decode`; the boundary at 4096 fires at the first decode step with head_sum at budget
+2048 = 128 prefix + 512 recent + 1408 scored. Every stage is compared with the oracle: prefill
+scores, the boundary's retained positions, table, req_to_token, relocated K/V/scores and freed
+slots (bit-exact, the oracle ranking the GPU's own pre-boundary scores), each step's attention
+output, and the accumulated scores after the last step.
+"""
+import sys
+import types
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from fakes import allocator, backend, layer
+
+pytestmark = pytest.mark.gpu
+
+PROMPT, CHUNK, STEPS = 4096, 2048, 256
+BUDGET, PREFIX, RECENT = 2048, 128, 512
+SCALE = 0.125
+ROW = 1
+
+
+@pytest.fixture(autouse=True)
+def fake_sglang(monkeypatch):
+    """The one SGLang import the hooks make (the SWA component id)."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    names = ["sglang", "sglang.srt", "sglang.srt.mem_cache", "sglang.srt.mem_cache.unified_cache",
+             "sglang.srt.mem_cache.unified_cache.component_type"]
+    for name in names:
+        monkeypatch.setitem(sys.modules, name, types.ModuleType(name))
+    sys.modules[names[-1]].ComponentType = SimpleNamespace(SWA="swa")
+    import gstar_evict
+    gstar_evict.STATE = None
+    yield gstar_evict
+    gstar_evict.STATE = None
+
+
+def _request(cfg, lengths):
+    """A request whose SWA cursor trails its current length by 128 tokens (gpt-oss's window)."""
+    req = SimpleNamespace(rid="r0", session=None, retraction_count=0,
+                          sampling_params=SimpleNamespace(custom_params={"gstar_eviction": cfg}))
+    req.kv = SimpleNamespace(req_pool_idx=ROW, get_evicted_seqlen=lambda kind: max(lengths[0] - 128, 0))
+    return req
+
+
+def _assert_same_positions(got, want, scores, slot_of):
+    """Retained positions equal; on a mismatch, name a head and the scores of what differs."""
+    if np.array_equal(got, want):
+        return
+    for g in range(got.shape[1]):
+        a, c = set(got[0, g].tolist()), set(want[0, g].tolist())
+        if a != c:
+            only_gpu, only_oracle = sorted(a - c)[:8], sorted(c - a)[:8]
+            sc = scores[0, g]
+            raise AssertionError(f"head {g}: kept only by the GPU {only_gpu} (scores "
+                                 f"{[float(sc[slot_of[x]]) for x in only_gpu]}), only by the oracle "
+                                 f"{only_oracle} (scores {[float(sc[slot_of[x]]) for x in only_oracle]})")
+    raise AssertionError("retained positions differ in order only")
+
+
+def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang):
+    ge = fake_sglang
+    g = torch.Generator().manual_seed(0)
+    slots_total = PROMPT + STEPS + 64
+    b = backend(rows=2, width=8192, slots=slots_total, layers=1, full=(0,), gen=g)
+    freed, alloc = allocator(slots=slots_total)
+    st = ge.state(b)
+    st.score_mode = "queue"
+    lay = layer(0, scaling=SCALE)
+    q_all = torch.randn((PROMPT + STEPS, 64, 64), generator=g).to(torch.bfloat16).cuda()
+    sinks = torch.randn(64, generator=g).to(torch.bfloat16).cuda()
+    slot_of = (torch.randperm(slots_total - 1, generator=g)[:PROMPT + STEPS] + 1).cuda()
+    keys, values = b.token_to_kv_pool.get_key_buffer(0), b.token_to_kv_pool.get_value_buffer(0)
+
+    cfg = {"name": "head_sum_2048", "budget": BUDGET, "prefix": PREFIX, "recent": RECENT, "seed": 0}
+    lengths = [0]
+    req = _request(cfg, lengths)
+    batch = SimpleNamespace(reqs=[req], tree_cache=SimpleNamespace(token_to_kv_pool_allocator=alloc))
+
+    ost = O.OracleState([keys.float().cpu().numpy()], [values.float().cpu().numpy()],
+                        st.req_to_token.cpu().numpy())
+    oe = O.live_entry(cfg)
+    kn, sn = ost.keys[0], sinks.float().cpu().numpy()
+    rows = torch.tensor([ROW], device="cuda")
+
+    # Prompt: two chunks; the chunk at 2048 triggers a boundary with nothing to evict.
+    for start in range(0, PROMPT, CHUNK):
+        new = slot_of[start:start + CHUNK]
+        st.req_to_token[ROW, start:start + CHUNK] = new.int()
+        ost.req_to_token[ROW, start:start + CHUNK] = new.cpu().numpy()
+        lengths[0] = start
+        req.extend_range = SimpleNamespace(start=start, length=CHUNK)
+        ge.on_extend(batch)
+        if start:
+            ofreed = []
+            O.boundary(ost, ROW, oe, start, start - 128, free=ofreed.append)
+        prefix = torch.zeros(start + 1, dtype=torch.int32, device="cuda")
+        b.kv_indptr.zero_()
+        ge.fill(b, 1, torch.tensor([start], device="cuda"), rows, prefix)
+        b.forward_metadata = SimpleNamespace(qo_indptr=torch.tensor([0, CHUNK], device="cuda"),
+                                             kv_indptr=b.kv_indptr[:2].clone(), kv_indices=prefix[:start])
+        fb = SimpleNamespace(req_pool_indices=rows, out_cache_loc=new, extend_prefix_lens_cpu=[start])
+        ge.after_extend(b, q_all[start:start + CHUNK].reshape(CHUNK, -1), lay, fb, sinks)
+        # Oracle chunk scores, 256 queries at a time (the probability tile stays small).
+        pre = slot_of[:start].cpu().numpy()
+        for lo in range(0, CHUNK, 256):
+            upd, sl = O.prefill_score_update(1, q_all[start + lo:start + lo + 256].float().cpu().numpy(), kn, sn,
+                                             SCALE, 8, np.concatenate((pre, new[:lo].cpu().numpy())),
+                                             new[lo:lo + 256].cpu().numpy())
+            ost.scores[0][:, sl] += upd.astype(np.float32)
+    entry = st.entries[ROW]
+    assert [ev["after"] for ev in entry["events"]] == [CHUNK] == [ev["after"] for ev in oe["events"]]
+    torch.testing.assert_close(st.scores.cpu(), torch.tensor(ost.scores), rtol=2e-3, atol=1e-6)
+
+    outs, want_outs = [], []
+    for t in range(STEPS):
+        p = PROMPT + t
+        lengths[0] = p
+        if t == 0:
+            # The oracle ranks the GPU's own pre-boundary scores, so selection compares bit-exactly.
+            ost.scores = st.scores.cpu().numpy().copy()
+            pre_scores = ost.scores.copy()
+        ge.on_decode(SimpleNamespace(reqs=[req], seq_lens_cpu=torch.tensor([p]),
+                                     tree_cache=SimpleNamespace(token_to_kv_pool_allocator=alloc)))
+        if t == 0:
+            ofreed = []
+            O.boundary(ost, ROW, oe, p, p - 128, free=ofreed.append)
+            torch.cuda.synchronize()
+            assert entry["count"] == oe["count"] == BUDGET
+            _assert_same_positions(entry["pos"].cpu().numpy(), oe["pos"], pre_scores, slot_of.cpu().numpy())
+            assert np.array_equal(st.table[ROW, :BUDGET].cpu().numpy(), ost.table[ROW, :BUDGET])
+            assert np.array_equal(st.req_to_token[ROW].cpu().numpy(), ost.req_to_token[ROW])
+            assert np.array_equal(keys.float().cpu().numpy(), ost.keys[0])
+            assert np.array_equal(values.float().cpu().numpy(), ost.values[0])
+            assert np.array_equal(st.scores.cpu().numpy(), ost.scores)
+            assert np.array_equal(torch.cat(freed).cpu().numpy(), ofreed[0])
+        # SGLang's allocation of the new token, then the CSR and the fused decode.
+        new = slot_of[p:p + 1]
+        st.req_to_token[ROW, p] = new.int()
+        ost.req_to_token[ROW, p] = int(new)
+        kv_indices = torch.zeros(p + 1, dtype=torch.int32, device="cuda")
+        ge.fill(b, 1, torch.tensor([p + 1], device="cuda"), rows, kv_indices)
+        b.forward_metadata = SimpleNamespace(kv_indptr=b.kv_indptr[:2], kv_indices=kv_indices)
+        fb = SimpleNamespace(out_cache_loc=new, req_pool_indices=rows, seq_lens_cpu=torch.tensor([p + 1]))
+        o = torch.empty((1, 64, 64), dtype=torch.bfloat16, device="cuda")
+        assert ge.decode(b, q_all[p:p + 1].reshape(1, -1), lay, fb, sinks, o.reshape(1, -1))
+        outs.append(o[0])
+        # Oracle step: the resident list is the table then the tail (R:136-152).
+        res = np.concatenate((ost.table[ROW, :oe["count"]], ost.req_to_token[ROW, oe["frontier"]:p + 1]))
+        qn = q_all[p].float().cpu().numpy()
+        want_o, norm = O.decode_attention(qn, ost.keys[0], ost.values[0], res, sn, SCALE)
+        ost.scores[:, :, int(new)] = 0.0
+        O.decode_scores_into(ost.scores[0], qn, ost.keys[0], res, norm, SCALE, 1)
+        want_outs.append(want_o)
+    ge.flush(st)
+    got = torch.stack(outs).float().cpu().numpy()
+    want = np.stack(want_outs)
+    np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2)
+    assert np.abs(got - want).mean() < 2e-3
+    torch.testing.assert_close(st.scores.cpu(), torch.tensor(ost.scores), rtol=2e-3, atol=1e-6)
