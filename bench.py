@@ -32,7 +32,7 @@ PAGE = 16
 PEAK_HBM_GBS = 8000.0
 
 
-def parse():
+def parse(argv=None):
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=512)
@@ -47,6 +47,8 @@ def parse():
     p.add_argument("--max-len", type=int, default=65536)
     p.add_argument("--policy", default="head_sum_2048")
     p.add_argument("--heavy", type=float, default=0.02)
+    p.add_argument("--dup", type=float, default=0.0,
+                   help="fraction of each layer's slots whose K row is an exact copy of another slot's")
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--kernel-reps", type=int, default=20, help="launches timed per layer for the roofline")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -54,7 +56,7 @@ def parse():
     p.add_argument("--copy-mib", type=int, default=0,
                    help="only run a plain device copy of this many MiB (5 launches): the byte-counter "
                         "calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE runs")
-    return p.parse_args()
+    return p.parse_args(argv)
 
 
 def decode_bytes(n_resident):
@@ -129,6 +131,11 @@ class Workload:
                 idx = torch.randint(1, slots, (nh,), device=dev, generator=gen)
                 kk = k[idx, h].float()
                 k[idx, h] = (4 * kk.norm(dim=-1, keepdim=True) * u[h]).to(torch.bfloat16)
+            if args.dup > 0:
+                nd = int(args.dup * slots)
+                dst = torch.randperm(slots - 1, device=dev, generator=gen)[:nd] + 1
+                src = torch.randint(1, slots, (nd,), device=dev, generator=gen)
+                k[dst] = k[src]
             keys[l], values[l] = k, v
         pool = SimpleNamespace(layers_mapping={l: (l, False) for l in range(L)},
                                get_key_buffer=keys.__getitem__, get_value_buffer=values.__getitem__)
@@ -277,8 +284,8 @@ def kernel_roofline(w, reps):
 
 def cpu_baseline(w):
     """Time the numpy oracle on a bounded sample of the same workload (2 sequences x 2 layers
-    decode at their real resident sets, one row-boundary's selection on 2 layers) and scale
-    to the full step (32 sequences x 12 layers, plus the measured boundary rate)."""
+    decode at their real resident sets, one row boundary on 2 layers) and scale to the full
+    step (bs sequences x 12 layers, plus the measured boundary rate)."""
     import numpy as np
     import oracle as O
     torch, a = w.torch, w.args
@@ -302,24 +309,37 @@ def cpu_baseline(w):
             O.decode_scores_into(sc, q, keys, local, norm, D ** -0.5, 1)
             t_dec += time.perf_counter() - t0
     per_seq_layer = t_dec / (seqs * layers)
-    # Boundary selection sample: the largest row's [2 layers, 8 heads, N] ranking.
+    # Boundary sample: the largest row's candidates on 2 layers, selection + relocation + repack
+    # (O.boundary) on a local pool holding just the row's candidate slots (local slot j + 1).
     i = max(range(a.bs), key=lambda j: w.resident(j))
     e = w.entries[i]
-    N = w.resident(i)
-    pos = np.concatenate((e["pos"][:layers].cpu().numpy() if e["count"] else np.zeros((layers, HKV, 0), np.int32),
-                          np.broadcast_to(np.arange(e["frontier"], w.lens[i]), (layers, HKV, w.lens[i] - e["frontier"]))),
-                         -1)
-    score = np.random.default_rng(0).random(pos.shape)
+    row, c, f, n = i + 1, e["count"], e["frontier"], w.lens[i]
+    N = c + n - f
+    slots = torch.cat((st.table[row, :c], st.req_to_token[row, f:n])).long()
+    pad = np.zeros((1, HKV, D), np.float32)
+    keys = [np.concatenate((pad, w.backend.token_to_kv_pool.get_key_buffer(l)[slots].float().cpu().numpy()))
+            for l in range(layers)]
+    vals = [np.concatenate((pad, w.backend.token_to_kv_pool.get_value_buffer(l)[slots].float().cpu().numpy()))
+            for l in range(layers)]
+    r2t = np.zeros((1, n + 1), np.int64)
+    r2t[0, f:n] = np.arange(c + 1, N + 1)
+    ost = O.OracleState(keys, vals, r2t, np.random.default_rng(0).random((layers, HKV, N + 1)).astype(np.float32))
+    ost.table[0, :c] = np.arange(1, c + 1)
+    oe = O.live_entry({"name": a.policy, "budget": a.budget, "prefix": a.prefix, "recent": a.recent,
+                       "seed": a.seed})
+    oe.update(frontier=f, count=c)
+    if c:
+        oe["pos"] = e["pos"][:layers].cpu().numpy().astype(np.int64)
     t0 = time.perf_counter()
-    O.choose(a.policy, pos, w.lens[i] + (a.interval - w.lens[i] % a.interval), a.budget, a.prefix, a.recent, score)
+    O.boundary(ost, 0, oe, n, None, free=lambda leftover: None)
     t_sel = (time.perf_counter() - t0) * a.layers / layers
     rate = w.boundaries / max(a.steps, 1)
     us_step = 1e6 * (per_seq_layer * a.bs * a.layers + rate * t_sel)
     return {"value": us_step, "unit": "us/step", "cores": 1, "kind": "port",
             "sample": f"numpy float64 oracle: decode attention + head_sum scores for {seqs} sequences x {layers} "
                       f"layers at their resident sets ({per_seq_layer * 1e3:.0f} ms each) scaled to {a.bs} x "
-                      f"{a.layers}; one {N}-column selection on {layers} layers scaled to {a.layers} layers at "
-                      f"{rate:.2f} boundaries/step"}
+                      f"{a.layers}; one {N}-candidate boundary (selection, K/V/score relocation, repack) on "
+                      f"{layers} layers scaled to {a.layers} layers at {rate:.2f} boundaries/step"}
 
 
 def measured_traffic():
@@ -350,6 +370,18 @@ def copy_calibration(torch, mib):
     ms = start.elapsed_time(end) / 5
     print(json.dumps({"copy_bytes": n, "read_plus_write_GBs": round(2 * n / (ms * 1e-3) / 1e9, 1),
                       "avg_ms": round(ms, 4)}), flush=True)
+
+
+def workload_name(args):
+    k = lambda n: f"{n // 1024}K" if n % 1024 == 0 else str(n)
+    scored = args.budget - args.prefix - args.recent
+    name = (f"gpt-oss-20b full-attention decode, {args.layers} layers, bs={args.bs}, lengths "
+            f"U[{k(args.min_len)},{k(args.max_len)}], budget {args.budget} ({args.prefix}+{args.recent}+{scored}), "
+            f"{args.policy.replace('_2048', '')}, evict every {args.interval} step{'s' if args.interval > 1 else ''}, "
+            f"16-token pages, {args.heavy * 100:g}% heavy hitters")
+    if args.dup:
+        name += f", {args.dup * 100:g}% duplicate keys"
+    return name
 
 
 def main():
@@ -383,24 +415,26 @@ def main():
     gbs = w.bytes / (gpu_ms / 1000) / 1e9
     per_launch, avg_us = kernel_roofline(w, args.kernel_reps)
     achieved = per_launch / (avg_us * 1e-6) / 1e9
-    traffic = measured_traffic()
+    # The committed counter summary covers the default workload only.
+    traffic = measured_traffic() if workload_name(args) == workload_name(parse([])) else None
     result = {
         "metric": "fused attn+score+evict µs/decode-step & HBM GB/s (% peak), bs=32, 32K budget",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4), "us_per_step": round(1000 * ms_step, 1), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "gpt-oss-20b full-attention decode, 12 layers, bs=32, lengths U[16K,64K], "
-                               "budget 32768 (512+4096+28160), head_sum, evict every 64 steps, 16-token pages, "
-                               "2% heavy hitters",
+        "config": {"workload": workload_name(args),
                    "batch": args.bs, "layers": args.layers, "budget": args.budget, "interval": args.interval,
                    "policy": args.policy, "score_mode": "eager" if args.eager else "queue",
                    "mean_resident": round(statistics.mean(w.resident_hist), 1),
                    "boundaries": w.boundaries, "wall_s": round(wall, 3)},
-        "roofline": {"bound": "hbm", "kernel": "decode_fused_kernel+decode_merge_kernel (one layer, bs=32)",
+        "roofline": {"bound": "hbm", "kernel": f"decode_fused_kernel+decode_merge_kernel (one layer, bs={args.bs})",
                      "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": per_launch, "avg_launch_us": round(avg_us, 2)},
         "step_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+        # Everything a step adds to its decode attention (score flush, selection, compaction, CSR
+        # fill, host waits), relative to the attention launches alone.
+        "evict_overhead_vs_attention": round((1000 * ms_step - args.layers * avg_us) / (args.layers * avg_us), 4),
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
