@@ -53,6 +53,9 @@ def parse(argv=None):
     p.add_argument("--kernel-reps", type=int, default=20, help="launches timed per layer for the roofline")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--eager", action="store_true", help="score each step eagerly (second K pass per step)")
+    p.add_argument("--prefill", action="store_true",
+                   help="time the chunked-prefill score tiles instead: 12 layers, 79,720-token prompt in "
+                        "8192-token chunks, prefix capped at the 28,672-token budget (MFMA roofline)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="only run a plain device copy of this many MiB (5 launches): the byte-counter "
                         "calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE runs")
@@ -372,6 +375,79 @@ def copy_calibration(torch, mib):
                       "avg_ms": round(ms, 4)}), flush=True)
 
 
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def prefill_bench(args, torch, ge):
+    """Chunked-prefill scoring at the 79,720-token shape: per chunk and layer, exact causal
+    softmax probabilities (sink in the normaliser) summed per KV head onto the keys' scores.
+    Algorithmic work = 2 * 64 heads * 64 dims flop per causal (query, key) pair for one QK^T
+    pass; the kernel issues a second pass (the normaliser first, then the probabilities)."""
+    prompt, chunk, cap = 79720, 8192, 512 + 4096 + 24064
+    L = args.layers
+    slots = cap + chunk + 64
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    keys, values = {}, {}
+    for l in range(L):
+        k = torch.randn((slots, HKV, D), device="cuda", dtype=torch.bfloat16, generator=g)
+        u = torch.randn((HKV, D), device="cuda", generator=g)
+        u = u / u.norm(dim=-1, keepdim=True)
+        heavy = torch.rand((slots, HKV), device="cuda", generator=g) < 0.05
+        planted = (4 * k.float().norm(dim=-1, keepdim=True) * u[None]).to(torch.bfloat16)
+        keys[l] = torch.where(heavy[..., None], planted, k)
+        values[l] = keys[l]  # values are not read by the score pass
+    pool = SimpleNamespace(layers_mapping={l: (l, False) for l in range(L)},
+                           get_key_buffer=keys.__getitem__, get_value_buffer=values.__getitem__)
+    backend = SimpleNamespace(token_to_kv_pool=pool, max_kv_splits=16,
+                              req_to_token_pool=SimpleNamespace(req_to_token=torch.zeros((2, 64), dtype=torch.int32,
+                                                                                         device="cuda")),
+                              kv_indptr=torch.zeros(3, dtype=torch.int32, device="cuda"))
+    ge.STATE = None
+    st = ge.state(backend)
+    q = torch.randn((chunk, HQ, D), device="cuda", dtype=torch.bfloat16, generator=g)
+    sinks = torch.randn(HQ, device="cuda", generator=g)
+    perm = torch.randperm(slots - 1, device="cuda", generator=g) + 1
+    layer_objs = [SimpleNamespace(sliding_window_size=-1, tp_q_head_num=HQ, tp_k_head_num=HKV, qk_head_dim=D,
+                                  layer_id=l, scaling=D ** -0.5) for l in range(L)]
+    plan = []  # (prefix, count) per chunk; the resident prefix is capped at the budget
+    for start in range(0, prompt, chunk):
+        plan.append((min(start, cap), min(chunk, prompt - start)))
+
+    def run():
+        for prefix, count in plan:
+            for l in range(L):
+                ge._prefill_scores(st, l, 1, layer_objs[l], q[:count], keys[l], sinks, perm[:prefix],
+                                   perm[prefix:prefix + count])
+
+    run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = max(1, min(args.steps, 3))  # one step is the whole 79,720-token prompt (about a second)
+    start.record()
+    for _ in range(reps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    pairs = sum(prefix * count + count * (count + 1) // 2 for prefix, count in plan)
+    flop = L * pairs * 2 * HQ * D
+    tflops = flop / (ms * 1e-3) / 1e12
+    return {
+        "metric": "chunked-prefill score tiles, TFLOP/s (one QK^T pass) and % of bf16 MFMA peak",
+        "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"gpt-oss-20b chunked prefill scoring, {L} layers, 79,720-token prompt in 8192-token "
+                               f"chunks, prefix capped at {cap} (512+4096+24064), head_sum, 5% heavy-hitter keys",
+                   "causal_pairs_per_layer": pairs},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "issued_frac": round(2 * tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        # Two exponentials per (query head, key) pair (normaliser pass, probability pass).
+        "exp2_T_per_s": round(2 * L * pairs * HQ / (ms * 1e-3) / 1e12, 2),
+    }
+
+
 def workload_name(args):
     k = lambda n: f"{n // 1024}K" if n % 1024 == 0 else str(n)
     scored = args.budget - args.prefix - args.recent
@@ -397,6 +473,9 @@ def main():
         sys.exit(1)
     if args.copy_mib:
         copy_calibration(torch, args.copy_mib)
+        return
+    if args.prefill:
+        print(json.dumps(prefill_bench(args, torch, ge)), flush=True)
         return
     w = Workload(args, torch, ge)
     for _ in range(args.warmup):
