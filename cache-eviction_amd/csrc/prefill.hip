@@ -8,7 +8,14 @@
 //   S = Q . K^T   [16 rows x 16 keys] per row-block and key-block (16x16x32 bf16)
 // Pass 1 streams the visible keys once to get each row's log-sum-exp (with the
 // sink); pass 2 streams them again, turns logits into probabilities with that
-// normaliser and accumulates column sums, one atomic add per key per workgroup.
+// normaliser and accumulates column sums.
+//
+// Work per (query head, key) is one exp2 per pass, which bounds the kernel (v_exp_f32 runs
+// at half the rate of an FMA): pass 1 keeps a lazily rescaled running maximum per row (one
+// FMA + exp2 + add per logit), pass 2 one FMA + exp2 + add. K tiles of 64 keys go through
+// LDS, double-buffered, one global load per workgroup per tile; column sums accumulate
+// in-lane over the wave's 16 queries, then in an LDS ring of 16 tiles that is added to the
+// scores once per ring. Query blocks are dispatched heaviest (longest causal range) first.
 #include "common.hpp"
 #include "host.hpp"
 
@@ -17,9 +24,15 @@ namespace gse {
 namespace pf {
 constexpr int D = 64;
 constexpr int GROUP = 8;
-constexpr int QB = 64;     // queries per workgroup
-constexpr int RB = 8;      // row-blocks per wave (16 queries)
-constexpr int KT = 64;     // keys per tile (4 key-blocks of 16)
+constexpr int QB = 64;          // queries per workgroup
+// Row-blocks (2 queries each) per wave: pass 1 keeps a running maximum and sum per row, so it
+// runs 8 waves of 4 row-blocks; pass 2 keeps one normaliser per row and runs 4 waves of 8.
+template <int PASS> constexpr int rows_per_wave() { return PASS == 1 ? 4 : 8; }
+template <int PASS> constexpr int waves() { return QB / (2 * rows_per_wave<PASS>()); }
+constexpr int KT = 64;          // keys per tile (4 key-blocks of 16)
+constexpr int KROW = D + 8;     // padded bf16 row of a staged key
+constexpr int RING = 16;        // tiles of column sums held before they are added to the scores
+constexpr float RESCALE = 8.f;  // a row's reference maximum moves when a logit exceeds it by 2^8
 }  // namespace pf
 
 struct PrefillArgs {
@@ -41,18 +54,91 @@ struct PrefillArgs {
   float* norm2;  // [count, q_heads] row normalisers in log2 units (sink included)
 };
 
-template <int PASS>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+// One 64-key tile of a wave: row-block rb's MFMAs for four 16-key blocks, then per logit one
+// FMA + exp2 (+ the add). Row-block rb + 1's MFMAs are issued before rb's exponentials.
+// MASKED: key (t0 + 16*kb + col) is dead for this lane's query 2*rb + grp/2 when
+// rel + 16*kb > 2*rb + grp/2, with rel = t0 + col - (position of the wave's first query).
+template <int PASS, bool MAX_MODE, bool MASKED, int RB>
+GSE_DEVICE void prefill_tile(const bf16x8_t (&qa)[RB][2], const bf16x8_t (&kb0)[4], const bf16x8_t (&kb1)[4],
+                             float (&ref)[RB][4], float (&sum)[RB][4], float (&cs)[4], float scale2,
+                             int64_t rel, int grp) {
   using namespace pf;
-  __shared__ float colsum[KT];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  f32x4_t dn[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    dn[kb] = mfma16x16x32(qa[0][0], kb0[kb], f32x4_t{0.f, 0.f, 0.f, 0.f});
+    dn[kb] = mfma16x16x32(qa[0][1], kb1[kb], dn[kb]);
+  }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    f32x4_t d[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) d[kb] = dn[kb];
+    if (rb + 1 < RB) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        dn[kb] = mfma16x16x32(qa[rb + 1][0], kb0[kb], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        dn[kb] = mfma16x16x32(qa[rb + 1][1], kb1[kb], dn[kb]);
+      }
+    }
+    if (MASKED) {
+      const int64_t qrel = 2 * rb + (grp >> 1);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        if (rel + 16 * kb > qrel)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) d[kb][r] = -INFINITY;
+    }
+    if (PASS == 1) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float tmax = fmaxf(fmaxf(d[0][r], d[1][r]), fmaxf(d[2][r], d[3][r])) * scale2;
+        if (tmax > ref[rb][r] + RESCALE) {  // rare after the first tiles
+          sum[rb][r] *= fast_exp2(ref[rb][r] - tmax);
+          ref[rb][r] = tmax;
+        }
+        const float e0 = fast_exp2(fmaf(d[0][r], scale2, -ref[rb][r]));
+        const float e1 = fast_exp2(fmaf(d[1][r], scale2, -ref[rb][r]));
+        const float e2 = fast_exp2(fmaf(d[2][r], scale2, -ref[rb][r]));
+        const float e3 = fast_exp2(fmaf(d[3][r], scale2, -ref[rb][r]));
+        sum[rb][r] += (e0 + e1) + (e2 + e3);
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const float p0 = fast_exp2(fmaf(d[kb][0], scale2, -ref[rb][0]));
+        const float p1 = fast_exp2(fmaf(d[kb][1], scale2, -ref[rb][1]));
+        const float p2 = fast_exp2(fmaf(d[kb][2], scale2, -ref[rb][2]));
+        const float p3 = fast_exp2(fmaf(d[kb][3], scale2, -ref[rb][3]));
+        if (MAX_MODE)
+          cs[kb] += xor16_max(fmaxf(fmaxf(p0, p1), fmaxf(p2, p3)));
+        else
+          cs[kb] += (p0 + p1) + (p2 + p3);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int PASS, bool MAX_MODE>
+__global__ __launch_bounds__(64 * pf::waves<PASS>()) void prefill_kernel(PrefillArgs a) {
+  using namespace pf;
+  constexpr int RB = rows_per_wave<PASS>();
+  constexpr int WAVES = waves<PASS>();
+  __shared__ __attribute__((aligned(16))) uint16_t ktile[2][KT * KROW];
+  __shared__ float ring[PASS == 2 ? RING * KT : 1];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int g = blockIdx.y;
-  const int64_t qb0 = int64_t(blockIdx.x) * QB;
-  const int64_t i0 = qb0 + 16 * wave;  // this wave's first query
-  // Keys visible to any query of the workgroup: CSR columns <= prefix_len + last query.
+  // Heaviest query blocks first: linear block i -> KV head i % kv_heads, query block from the end.
+  const int64_t nqb = (a.count + QB - 1) / QB;
+  const int g = blockIdx.x % a.kv_heads;
+  const int64_t qb0 = (nqb - 1 - int64_t(blockIdx.x / a.kv_heads)) * QB;
+  const int64_t i0 = qb0 + 2 * RB * wave;  // this wave's first query
   const int64_t last_q = (qb0 + QB < a.count ? qb0 + QB : a.count) - 1;
-  const int64_t kend = a.prefix_len + last_q + 1 < a.total ? a.prefix_len + last_q + 1 : a.total;
+  const int64_t kend = a.prefix_len + last_q + 1;  // keys any query of the workgroup sees
+  const bool wave_live = i0 < a.count;
+  const int64_t wave_kend = a.prefix_len + (i0 + 2 * RB - 1 < a.count ? i0 + 2 * RB - 1 : a.count - 1) + 1;
 
   // A fragments: row col of row-block rb is query i0 + 2*rb + col/8, head g*8 + col%8;
   // lane supplies dims [16*grp, 16*grp + 16) as two 8-dim MFMA halves.
@@ -60,129 +146,115 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int64_t qi = i0 + 2 * rb + col / 8;
+    qa[rb][0] = bf16x8_t{};
+    qa[rb][1] = bf16x8_t{};
     if (qi < a.count) {
       const uint16_t* qp = a.q + qi * a.q_st + int64_t(g * GROUP + col % 8) * a.q_sh + 16 * grp;
       qa[rb][0] = as_bf16x8(*reinterpret_cast<const uint4*>(qp));
       qa[rb][1] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 8));
-    } else {
-      qa[rb][0] = bf16x8_t{};
-      qa[rb][1] = bf16x8_t{};
     }
   }
-  // Output rows of this lane in row-block rb: query i0 + 2*rb + grp/2, heads 4*(grp%2) + r.
+  // This lane's output rows in row-block rb: query i0 + 2*rb + grp/2, heads hq0 + r.
   const int hq0 = g * GROUP + 4 * (grp & 1);
-
-  float m[RB][4], l[RB][4], nrm[RB][4];
+  // Pass 1: per-row reference maximum (log2 units) and the sum of 2^(x - ref) over this lane's
+  // keys. Pass 2: the rows' normalisers (+inf for rows past the chunk: their terms are 0).
+  float ref[RB][4], sum[RB][4];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int rb = 0; rb < RB; ++rb) {
+    const int64_t qi = i0 + 2 * rb + (grp >> 1);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      m[rb][r] = -INFINITY;
-      l[rb][r] = 0.f;
-      nrm[rb][r] = 0.f;
+      ref[rb][r] = -1e30f;  // finite, so fully masked rows give 2^(-inf) = 0, never NaN
+      sum[rb][r] = 0.f;
+      if (PASS == 2) ref[rb][r] = qi < a.count ? a.norm2[qi * a.q_heads + hq0 + r] : INFINITY;
     }
-  if (PASS == 2) {
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int64_t qi = i0 + 2 * rb + (grp >> 1);
-      if (qi < a.count)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) nrm[rb][r] = a.norm2[qi * a.q_heads + hq0 + r];
-    }
-    if (threadIdx.x < KT) colsum[threadIdx.x] = 0.f;
-    __syncthreads();
   }
-  const bool max_mode = a.mode == 2;
+  if (PASS == 2)
+    for (int t = threadIdx.x; t < RING * KT; t += blockDim.x) ring[t] = 0.f;
 
-  for (int64_t t0 = 0; t0 < kend; t0 += KT) {
-    // B fragments: key t0 + 16*kb + col, dims [16*grp, 16*grp + 16).
-    uint4 kf[4][2];
-    int64_t slot[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int64_t key = t0 + 16 * kb + col;
-      slot[kb] = key < kend ? load_index_dyn(a.slots, a.slots_dtype, key) : 0;
-      const uint16_t* kp = a.k + slot[kb] * a.kv_ss + int64_t(g) * a.kv_sh + 16 * grp;
-      kf[kb][0] = *reinterpret_cast<const uint4*>(kp);
-      kf[kb][1] = *reinterpret_cast<const uint4*>(kp + 8);
-    }
-    // Causal mask is needed only where the tile reaches past this wave's first query.
-    const bool need_mask = t0 + KT - 1 > a.prefix_len + i0 || t0 + KT > kend;
-    float cs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int64_t qi = i0 + 2 * rb + (grp >> 1);
-      const int64_t qpos = a.prefix_len + qi;
-      const bool row_dead = qi >= a.count;  // rows past the chunk carry zero queries
-      float x[4][4];
+  // Cooperative tile load: thread t < 256 stages key t/4, dims [16*(t%4), +16).
+  const bool loader = threadIdx.x < 256;
+  const int lk = (threadIdx.x >> 2) & 63, lp = threadIdx.x & 3;
+  auto load_tile = [&](int64_t t0, uint4& x0, uint4& x1) {
+    const int64_t key = t0 + lk;
+    const int64_t s = key < kend ? load_index_dyn(a.slots, a.slots_dtype, key) : 0;
+    const auto kp = as_global(a.k) + s * a.kv_ss + int64_t(g) * a.kv_sh + 16 * lp;
+    x0 = gload16(kp);
+    x1 = gload16(kp + 8);
+  };
+  auto store_tile = [&](int buf, uint4 x0, uint4 x1) {
+    uint16_t* dst = &ktile[buf][lk * KROW + 16 * lp];
+    *reinterpret_cast<uint4*>(dst) = x0;
+    *reinterpret_cast<uint4*>(dst + 8) = x1;
+  };
+  const int ntiles = int((kend + KT - 1) / KT);
+  uint4 x0 = {}, x1 = {};
+  if (loader) {
+    load_tile(0, x0, x1);
+    store_tile(0, x0, x1);
+  }
+  __syncthreads();
+
+#pragma unroll 1
+  for (int ti = 0; ti < ntiles; ++ti) {
+    const int64_t t0 = int64_t(ti) * KT;
+    if (loader && ti + 1 < ntiles) load_tile(t0 + KT, x0, x1);  // in flight during this tile's compute
+    if (wave_live && t0 < wave_kend) {
+      const uint16_t* kt = ktile[ti & 1];
+      bf16x8_t kb0[4], kb1[4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mfma16x16x32(qa[rb][0], as_bf16x8(kf[kb][0]), acc);
-        acc = mfma16x16x32(qa[rb][1], as_bf16x8(kf[kb][1]), acc);
-        const int64_t key = t0 + 16 * kb + col;
-        const bool dead = row_dead || (need_mask && (key > qpos || key >= kend));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) x[kb][r] = dead ? -INFINITY : acc[r] * a.scale2;
+        const uint16_t* kr = kt + (16 * kb + col) * KROW + 16 * grp;
+        kb0[kb] = as_bf16x8(*reinterpret_cast<const uint4*>(kr));
+        kb1[kb] = as_bf16x8(*reinterpret_cast<const uint4*>(kr + 8));
       }
-      if (PASS == 1) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float tm = fmaxf(fmaxf(x[0][r], x[1][r]), fmaxf(x[2][r], x[3][r]));
-          const float mn = fmaxf(m[rb][r], tm);
-          if (mn != -INFINITY) {
-            l[rb][r] = l[rb][r] * fast_exp2(m[rb][r] - mn) + fast_exp2(x[0][r] - mn) + fast_exp2(x[1][r] - mn) +
-                       fast_exp2(x[2][r] - mn) + fast_exp2(x[3][r] - mn);
-            m[rb][r] = mn;
-          }
-        }
-      } else {
+      // Keys past the wave's first query need the causal mask (at most the last two tiles).
+      float cs[4] = {0.f, 0.f, 0.f, 0.f};
+      const int64_t qpos0 = a.prefix_len + i0;
+      if (t0 + KT - 1 > qpos0)
+        prefill_tile<PASS, MAX_MODE, true, RB>(qa, kb0, kb1, ref, sum, cs, a.scale2, t0 + col - qpos0, grp);
+      else
+        prefill_tile<PASS, MAX_MODE, false, RB>(qa, kb0, kb1, ref, sum, cs, a.scale2, 0, grp);
+      if (PASS == 2) {
+        // Sum mode: every lane group holds partial sums; max mode: groups 0/1 hold the even
+        // queries' (twice), 2/3 the odd ones'.
+        float* rt = ring + (ti % RING) * KT;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-          float red = 0.f;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float p = fast_exp2(x[kb][r] - nrm[rb][r]);
-            red = max_mode ? fmaxf(red, p) : red + p;
-          }
-          // Heads 0-3 (groups 0, 2) with heads 4-7 (groups 1, 3) of the same query.
-          red = max_mode ? xor16_max(red) : xor16_sum(red);
-          cs[kb] += red;
+          const float tot = MAX_MODE ? xor32_sum(cs[kb]) : xor32_sum(xor16_sum(cs[kb]));
+          if (grp == 0) atomicAdd(&rt[16 * kb + col], tot);
         }
       }
     }
-    if (PASS == 2) {
-      // Groups 0/1 hold the even queries' sums, groups 2/3 the odd ones'.
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const float tot = xor32_sum(cs[kb]);
-        if (grp == 0 && t0 + 16 * kb + col < kend) atomicAdd(&colsum[16 * kb + col], tot);
-      }
-      __syncthreads();
-      if (threadIdx.x < KT) {
-        const int64_t key = t0 + threadIdx.x;
+    if (loader && ti + 1 < ntiles) store_tile((ti + 1) & 1, x0, x1);
+    __syncthreads();
+    if (PASS == 2 && ((ti + 1) % RING == 0 || ti + 1 == ntiles)) {
+      // Add the ring's tiles to the scores, one atomic per key per workgroup.
+      const int64_t base = int64_t(ti - ti % RING) * KT;
+      for (int t = threadIdx.x; t < RING * KT; t += blockDim.x) {
+        const int64_t key = base + t;
         if (key < kend) {
           const int64_t s = load_index_dyn(a.slots, a.slots_dtype, key);
-          unsafeAtomicAdd(&a.scores[int64_t(g) * a.ssg + s * a.sss], colsum[threadIdx.x]);
+          unsafeAtomicAdd(&a.scores[int64_t(g) * a.ssg + s * a.sss], ring[t]);
         }
-        colsum[threadIdx.x] = 0.f;
+        ring[t] = 0.f;
       }
       __syncthreads();
     }
   }
 
-  if (PASS == 1) {
-    // Combine each row's (m, l) over the 16 key columns, then fold in the sink.
+  if (PASS == 1 && wave_live) {
+    // Combine each row's (ref, sum) over the 16 key columns, then fold in the sink.
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float mm = m[rb][r], ll = l[rb][r];
+        float mm = ref[rb][r], ll = sum[rb][r];
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) {
           const float mo = __shfl_xor(mm, o, kWave), lo = __shfl_xor(ll, o, kWave);
           const float mn = fmaxf(mm, mo);
-          ll = (mm == -INFINITY ? 0.f : ll * fast_exp2(mm - mn)) + (mo == -INFINITY ? 0.f : lo * fast_exp2(mo - mn));
+          ll = ll * fast_exp2(mm - mn) + lo * fast_exp2(mo - mn);
           mm = mn;
         }
         const int64_t qi = i0 + 2 * rb + (grp >> 1);
@@ -225,9 +297,17 @@ extern "C" int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_s
                    prefix_len, sinks, sinks_dtype, mode, scores, scores_stride_g, scores_stride_s, q_heads, kv_heads,
                    sm_scale * kLog2e, static_cast<float*>(workspace)};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid(unsigned((count + pf::QB - 1) / pf::QB), unsigned(kv_heads));
-  hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(256), 0, s, a);
-  if (int rc = gse_launch_check("prefill pass 1")) return rc;
-  hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(256), 0, s, a);
+  const int64_t blocks = (count + pf::QB - 1) / pf::QB * kv_heads;
+  if (blocks >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "prefill: chunk too large");
+  const dim3 grid{static_cast<uint32_t>(blocks)};
+  if (mode == 2) {
+    hipLaunchKernelGGL((prefill_kernel<1, true>), grid, dim3(64 * pf::waves<1>()), 0, s, a);
+    if (int rc = gse_launch_check("prefill pass 1")) return rc;
+    hipLaunchKernelGGL((prefill_kernel<2, true>), grid, dim3(64 * pf::waves<2>()), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((prefill_kernel<1, false>), grid, dim3(64 * pf::waves<1>()), 0, s, a);
+    if (int rc = gse_launch_check("prefill pass 1")) return rc;
+    hipLaunchKernelGGL((prefill_kernel<2, false>), grid, dim3(64 * pf::waves<2>()), 0, s, a);
+  }
   return gse_launch_check("prefill pass 2");
 }
