@@ -90,13 +90,25 @@ GSE_DEVICE void prefill_tile(const bf16x8_t (&qa)[RB][2], const bf16x8_t (&kb0)[
           for (int r = 0; r < 4; ++r) d[kb][r] = -INFINITY;
     }
     if (PASS == 1) {
+      float tmax[4];
+      bool need = false;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float tmax = fmaxf(fmaxf(d[0][r], d[1][r]), fmaxf(d[2][r], d[3][r])) * scale2;
-        if (tmax > ref[rb][r] + RESCALE) {  // rare after the first tiles
-          sum[rb][r] *= fast_exp2(ref[rb][r] - tmax);
-          ref[rb][r] = tmax;
+        tmax[r] = fmaxf(fmaxf(d[0][r], d[1][r]), fmaxf(d[2][r], d[3][r])) * scale2;
+        need |= tmax[r] > ref[rb][r] + RESCALE;
+      }
+      // A wave-uniform branch, so the rescale's exponentials run only in the (rare) tiles
+      // where some row's maximum moved.
+      if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float nr = tmax[r] > ref[rb][r] + RESCALE ? tmax[r] : ref[rb][r];
+          sum[rb][r] *= fast_exp2(ref[rb][r] - nr);
+          ref[rb][r] = nr;
         }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
         const float e0 = fast_exp2(fmaf(d[0][r], scale2, -ref[rb][r]));
         const float e1 = fast_exp2(fmaf(d[1][r], scale2, -ref[rb][r]));
         const float e2 = fast_exp2(fmaf(d[2][r], scale2, -ref[rb][r]));
