@@ -16,6 +16,8 @@
 // LDS, double-buffered, one global load per workgroup per tile; column sums accumulate
 // in-lane over the wave's 16 queries, then in an LDS ring of 16 tiles that is added to the
 // scores once per ring. Query blocks are dispatched heaviest (longest causal range) first.
+#include <type_traits>
+
 #include "common.hpp"
 #include "host.hpp"
 
@@ -279,6 +281,210 @@ __global__ __launch_bounds__(64 * pf::waves<PASS>()) void prefill_kernel(Prefill
   }
 }
 
+// ---------------------------------------------------------------------------
+// Static regret diagnostic (pass 3)
+// ---------------------------------------------------------------------------
+constexpr int DIAG_MAX_SPECS = 8;
+
+struct DiagArgs {
+  PrefillArgs p;         // q, keys, slots, sinks, scale, row normalisers of pass 1
+  float* score_max;      // second score table (max over the KV head's query heads)
+  const uint32_t* evicted;  // bit k of word w of (spec s, KV head g): key 32*w + k is evicted
+  int n_specs;
+  int64_t ev_ss, ev_sg;  // word strides of spec and KV head
+  float* lost;           // lost[s * lost_ss + i] += ... for chunk query i
+  int64_t lost_ss;
+  float lost_scale;      // 1 / (query heads * full layers)
+};
+
+// Pass 3 of a diagnostic chunk: the exact probabilities of pass 1's normalisers, added to two
+// position-indexed score tables (sum and max over each KV head's query heads, summed over the
+// chunk's queries), and every spec's lost mass per query: the group-summed probability on
+// keys the spec has evicted, summed over keys and KV heads, times lost_scale. Geometry as pass 1
+// (8 waves x 4 row-blocks per workgroup of 64 queries); K tiles through LDS, column sums through
+// two LDS rings.
+__global__ __launch_bounds__(64 * pf::waves<1>()) void diagnose_kernel(DiagArgs da) {
+  using namespace pf;
+  const PrefillArgs& a = da.p;
+  constexpr int RB = rows_per_wave<1>();
+  __shared__ __attribute__((aligned(16))) uint16_t ktile[2][KT * KROW];
+  __shared__ float ring_sum[RING * KT], ring_max[RING * KT];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int64_t nqb = (a.count + QB - 1) / QB;
+  const int g = blockIdx.x % a.kv_heads;
+  const int64_t qb0 = (nqb - 1 - int64_t(blockIdx.x / a.kv_heads)) * QB;
+  const int64_t i0 = qb0 + 2 * RB * wave;
+  const int64_t last_q = (qb0 + QB < a.count ? qb0 + QB : a.count) - 1;
+  const int64_t kend = a.prefix_len + last_q + 1;
+  const bool wave_live = i0 < a.count;
+  const int64_t wave_kend = a.prefix_len + (i0 + 2 * RB - 1 < a.count ? i0 + 2 * RB - 1 : a.count - 1) + 1;
+
+  bf16x8_t qa[RB][2];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int64_t qi = i0 + 2 * rb + col / 8;
+    qa[rb][0] = bf16x8_t{};
+    qa[rb][1] = bf16x8_t{};
+    if (qi < a.count) {
+      const uint16_t* qp = a.q + qi * a.q_st + int64_t(g * GROUP + col % 8) * a.q_sh + 16 * grp;
+      qa[rb][0] = as_bf16x8(*reinterpret_cast<const uint4*>(qp));
+      qa[rb][1] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 8));
+    }
+  }
+  const int hq0 = g * GROUP + 4 * (grp & 1);
+  float nrm[RB][4];
+  float lost[DIAG_MAX_SPECS][RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int64_t qi = i0 + 2 * rb + (grp >> 1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) nrm[rb][r] = qi < a.count ? a.norm2[qi * a.q_heads + hq0 + r] : INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < DIAG_MAX_SPECS; ++sp) lost[sp][rb] = 0.f;
+  }
+  for (int t = threadIdx.x; t < RING * KT; t += blockDim.x) {
+    ring_sum[t] = 0.f;
+    ring_max[t] = 0.f;
+  }
+
+  const bool loader = threadIdx.x < 256;
+  const int lk = (threadIdx.x >> 2) & 63, lp = threadIdx.x & 3;
+  auto load_tile = [&](int64_t t0, uint4& x0, uint4& x1) {
+    const int64_t key = t0 + lk;
+    const int64_t s = key < kend ? load_index_dyn(a.slots, a.slots_dtype, key) : 0;
+    const auto kp = as_global(a.k) + s * a.kv_ss + int64_t(g) * a.kv_sh + 16 * lp;
+    x0 = gload16(kp);
+    x1 = gload16(kp + 8);
+  };
+  auto store_tile = [&](int buf, uint4 x0, uint4 x1) {
+    uint16_t* dst = &ktile[buf][lk * KROW + 16 * lp];
+    *reinterpret_cast<uint4*>(dst) = x0;
+    *reinterpret_cast<uint4*>(dst + 8) = x1;
+  };
+  const int ntiles = int((kend + KT - 1) / KT);
+  uint4 x0 = {}, x1 = {};
+  if (loader) {
+    load_tile(0, x0, x1);
+    store_tile(0, x0, x1);
+  }
+  __syncthreads();
+
+#pragma unroll 1
+  for (int ti = 0; ti < ntiles; ++ti) {
+    const int64_t t0 = int64_t(ti) * KT;
+    if (loader && ti + 1 < ntiles) load_tile(t0 + KT, x0, x1);
+    if (wave_live && t0 < wave_kend) {
+      const uint16_t* kt = ktile[ti & 1];
+      bf16x8_t kb0[4], kb1[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint16_t* kr = kt + (16 * kb + col) * KROW + 16 * grp;
+        kb0[kb] = as_bf16x8(*reinterpret_cast<const uint4*>(kr));
+        kb1[kb] = as_bf16x8(*reinterpret_cast<const uint4*>(kr + 8));
+      }
+      // Evicted bits of this lane's four keys, per spec (bit kb of ev[sp]).
+      uint32_t ev[DIAG_MAX_SPECS];
+#pragma unroll
+      for (int sp = 0; sp < DIAG_MAX_SPECS; ++sp) {
+        ev[sp] = 0;
+        if (sp < da.n_specs) {
+          const uint32_t* w = da.evicted + sp * da.ev_ss + int64_t(g) * da.ev_sg + (t0 >> 5);
+          const uint32_t w0 = w[0], w1 = w[1];
+          ev[sp] = ((w0 >> col) & 1u) | (((w0 >> (16 + col)) & 1u) << 1) | (((w1 >> col) & 1u) << 2) |
+                   (((w1 >> (16 + col)) & 1u) << 3);
+        }
+      }
+      const int64_t rel = t0 + col - (a.prefix_len + i0);
+      float cs[4] = {0.f, 0.f, 0.f, 0.f}, cm[4] = {0.f, 0.f, 0.f, 0.f};
+      // The causal mask only on the tiles that reach past the wave's first query.
+      auto rows = [&](auto masked_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          f32x4_t d[4];
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) {
+            d[kb] = mfma16x16x32(qa[rb][0], kb0[kb], f32x4_t{0.f, 0.f, 0.f, 0.f});
+            d[kb] = mfma16x16x32(qa[rb][1], kb1[kb], d[kb]);
+          }
+          if (MASKED) {
+            const int64_t qrel = 2 * rb + (grp >> 1);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+              if (rel + 16 * kb > qrel)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) d[kb][r] = -INFINITY;
+          }
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) {
+            const float p0 = fast_exp2(fmaf(d[kb][0], a.scale2, -nrm[rb][0]));
+            const float p1 = fast_exp2(fmaf(d[kb][1], a.scale2, -nrm[rb][1]));
+            const float p2 = fast_exp2(fmaf(d[kb][2], a.scale2, -nrm[rb][2]));
+            const float p3 = fast_exp2(fmaf(d[kb][3], a.scale2, -nrm[rb][3]));
+            const float psum = (p0 + p1) + (p2 + p3);
+            cs[kb] += psum;
+            cm[kb] += xor16_max(fmaxf(fmaxf(p0, p1), fmaxf(p2, p3)));
+#pragma unroll
+            for (int sp = 0; sp < DIAG_MAX_SPECS; ++sp)
+              if (sp < da.n_specs) lost[sp][rb] += (ev[sp] >> kb) & 1u ? psum : 0.f;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      if (t0 + KT - 1 > a.prefix_len + i0)
+        rows(std::true_type{});
+      else
+        rows(std::false_type{});
+      float* rs = ring_sum + (ti % RING) * KT;
+      float* rm = ring_max + (ti % RING) * KT;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const float tsum = xor32_sum(xor16_sum(cs[kb]));
+        const float tmax = xor32_sum(cm[kb]);
+        if (grp == 0) {
+          atomicAdd(&rs[16 * kb + col], tsum);
+          atomicAdd(&rm[16 * kb + col], tmax);
+        }
+      }
+    }
+    if (loader && ti + 1 < ntiles) store_tile((ti + 1) & 1, x0, x1);
+    __syncthreads();
+    if ((ti + 1) % RING == 0 || ti + 1 == ntiles) {
+      const int64_t base = int64_t(ti - ti % RING) * KT;
+      for (int t = threadIdx.x; t < RING * KT; t += blockDim.x) {
+        const int64_t key = base + t;
+        if (key < kend) {
+          // Diagnostic score tables are indexed by position (the chunk's CSR column).
+          unsafeAtomicAdd(&a.scores[int64_t(g) * a.ssg + key * a.sss], ring_sum[t]);
+          unsafeAtomicAdd(&da.score_max[int64_t(g) * a.ssg + key * a.sss], ring_max[t]);
+        }
+        ring_sum[t] = 0.f;
+        ring_max[t] = 0.f;
+      }
+      __syncthreads();
+    }
+  }
+
+  if (wave_live) {
+    // Per spec and query: the lane sums over its key columns (16 lanes) and the two head halves.
+#pragma unroll
+    for (int sp = 0; sp < DIAG_MAX_SPECS; ++sp) {
+      if (sp >= da.n_specs) break;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        float v = lost[sp][rb];
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, kWave);
+        v = xor16_sum(v);
+        const int64_t qi = i0 + 2 * rb + (grp >> 1);
+        if (col == 0 && (grp & 1) == 0 && qi < a.count) atomicAdd(&da.lost[sp * da.lost_ss + qi], v * da.lost_scale);
+      }
+    }
+  }
+}
+
 }  // namespace gse
 
 using namespace gse;
@@ -322,4 +528,48 @@ extern "C" int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_s
     hipLaunchKernelGGL((prefill_kernel<2, false>), grid, dim3(64 * pf::waves<2>()), 0, s, a);
   }
   return gse_launch_check("prefill pass 2");
+}
+
+extern "C" int gse_diagnose_chunk(const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t count,
+                                  const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_h, const void* slots,
+                                  int slots_dtype, int64_t total, int64_t prefix_len, const void* sinks,
+                                  int sinks_dtype, float* score_sum, float* score_max, int64_t scores_stride_g,
+                                  int64_t scores_stride_s, const uint32_t* evicted, int n_specs,
+                                  int64_t evicted_stride_s, int64_t evicted_stride_g, float* lost,
+                                  int64_t lost_stride_s, float lost_scale, int q_heads, int kv_heads, int head_dim,
+                                  float sm_scale, void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
+  if (head_dim != pf::D || kv_heads < 1 || q_heads != pf::GROUP * kv_heads)
+    return gse_fail(GSE_ESHAPE, "diagnose: need head_dim 64 and q_heads == 8 * kv_heads");
+  if (n_specs < 0 || n_specs > DIAG_MAX_SPECS) return gse_fail(GSE_EINVAL, "diagnose: 0..8 policy specs");
+  if (count < 0 || prefix_len < 0 || total != prefix_len + count)
+    return gse_fail(GSE_EINVAL, "diagnose: total must equal prefix_len + count");
+  if (count == 0) return GSE_OK;
+  if (q_stride_t % 8 || q_stride_h % 8 || kv_stride_s % 8 || kv_stride_h % 8)
+    return gse_fail(GSE_EINVAL, "diagnose: strides must be multiples of 8 elements");
+  if (!q || !k_pool || !slots || !sinks || !score_sum || !score_max || !lost || (n_specs && !evicted))
+    return gse_fail(GSE_EINVAL, "diagnose: null pointer");
+  if (evicted_stride_g * 32 < ((total + 63) / 64) * 64)
+    return gse_fail(GSE_EINVAL, "diagnose: evicted rows must cover the visible keys rounded up to 64");
+  if (workspace_bytes < gse_prefill_workspace_bytes(count, q_heads))
+    return gse_fail(GSE_EWORKSPACE, "diagnose: workspace too small");
+  DiagArgs da;
+  da.p = {static_cast<const uint16_t*>(q), q_stride_t, q_stride_h, count, static_cast<const uint16_t*>(k_pool),
+          kv_stride_s, kv_stride_h, slots, slots_dtype, total, prefix_len, sinks, sinks_dtype, 1, score_sum,
+          scores_stride_g, scores_stride_s, q_heads, kv_heads, sm_scale * kLog2e, static_cast<float*>(workspace)};
+  da.score_max = score_max;
+  da.evicted = evicted;
+  da.n_specs = n_specs;
+  da.ev_ss = evicted_stride_s;
+  da.ev_sg = evicted_stride_g;
+  da.lost = lost;
+  da.lost_ss = lost_stride_s;
+  da.lost_scale = lost_scale;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t blocks = (count + pf::QB - 1) / pf::QB * kv_heads;
+  if (blocks >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "diagnose: chunk too large");
+  const dim3 grid{static_cast<uint32_t>(blocks)};
+  hipLaunchKernelGGL((prefill_kernel<1, false>), grid, dim3(64 * pf::waves<1>()), 0, s, da.p);
+  if (int rc = gse_launch_check("diagnose pass 1")) return rc;
+  hipLaunchKernelGGL(diagnose_kernel, grid, dim3(64 * pf::waves<1>()), 0, s, da);
+  return gse_launch_check("diagnose pass 3");
 }

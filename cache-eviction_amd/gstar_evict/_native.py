@@ -47,6 +47,8 @@ SIGNATURES = {
     "gse_prefill_workspace_bytes": (_l, [_l, _i]),
     "gse_prefill_scores": (_i, [_p, _l, _l, _l, _p, _l, _l, _p, _i, _l, _l, _p, _i, _i, _p, _l, _l, _i, _i, _i,
                                 _f, _p, _l, _p]),
+    "gse_diagnose_chunk": (_i, [_p, _l, _l, _l, _p, _l, _l, _p, _i, _l, _l, _p, _i, _p, _p, _l, _l, _p, _i, _l,
+                                _l, _p, _l, _f, _i, _i, _i, _f, _p, _l, _p]),
 }
 
 _lock = threading.Lock()

@@ -265,6 +265,27 @@ int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_stride_h, in
                        int q_heads, int kv_heads, int head_dim, float sm_scale,
                        void* workspace, int64_t workspace_bytes, gse_stream_t stream);
 
+/*
+ * diagnose_chunk — one full layer of one prefill chunk of a static regret
+ * diagnostic (R:587-615, `_diagnose`), with the row normalisers of
+ * prefill_scores' first pass:
+ *   score_sum[g, k] += sum_i sum_{h in g} p[h, i, k]      (k = CSR position 0..total-1)
+ *   score_max[g, k] += sum_i max_{h in g} p[h, i, k]
+ *   lost[s, i]      += lost_scale * sum_g sum_k [evicted(s, g, k)] sum_{h in g} p[h, i, k]
+ * evicted: bit k%32 of word k/32 of row (s, g) (rows evicted_stride_g words,
+ * covering total rounded up to 64); lost points at the chunk's first query
+ * column; lost_scale = 1 / (q_heads * full layers). n_specs <= 8; same shape
+ * limits and workspace as prefill_scores.
+ */
+int gse_diagnose_chunk(const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t count,
+                       const void* k_pool, int64_t kv_stride_s, int64_t kv_stride_h,
+                       const void* slots, int slots_dtype, int64_t total, int64_t prefix_len,
+                       const void* sinks, int sinks_dtype, float* score_sum, float* score_max,
+                       int64_t scores_stride_g, int64_t scores_stride_s, const uint32_t* evicted, int n_specs,
+                       int64_t evicted_stride_s, int64_t evicted_stride_g, float* lost, int64_t lost_stride_s,
+                       float lost_scale, int q_heads, int kv_heads, int head_dim, float sm_scale,
+                       void* workspace, int64_t workspace_bytes, gse_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
