@@ -1,0 +1,100 @@
+"""Device state of the runtime: one object per SGLang scheduler (GPU).
+
+It holds the tensors the reference's State holds (R:89-110; same names, shapes and dtypes, since
+the hooks and tests read them) plus what this build adds: the decode score queues, cached
+workspaces and the per-layer K/V pointer tables of the boundary kernels.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+
+class State:
+    """Per-row eviction state (``frontier``, ``count``, ``mode``, the shared slot ``table``), the
+    per-(full layer, KV head, slot) fp32 ``scores``, the request ``entries`` by row, and the
+    queued decode steps (``qq``/``qnorm``/``qlim``/``qcount`` per full layer and row; ``queued``
+    mirrors the count on the host)."""
+
+    def __init__(self, backend):
+        pool = backend.token_to_kv_pool
+        r2t = backend.req_to_token_pool.req_to_token
+        self.pool, self.req_to_token, self.device = pool, r2t, r2t.device
+        n_rows, width = r2t.shape
+        # Full-attention layers in layer order; sliding-window layers keep SGLang's own cache.
+        self.full_layers = [lid for lid in sorted(pool.layers_mapping) if not pool.layers_mapping[lid][1]]
+        self.index = dict(zip(self.full_layers, range(len(self.full_layers))))
+        self.first_full = self.full_layers[0]
+        self.num_slots, self.kv_heads, self.dim = (int(x) for x in pool.get_key_buffer(self.first_full).shape)
+        i32 = dict(dtype=torch.int32, device=self.device)
+        self.frontier, self.count, self.mode = (torch.zeros(n_rows, **i32) for _ in range(3))
+        self.table = torch.zeros((n_rows, width), **i32)
+        # [layer, head, slot] view of [layer, slot, head] storage: one slot's 8 head scores are
+        # adjacent, so the kernels touch a 32-byte row per slot.
+        backing = torch.zeros((len(self.full_layers), self.num_slots, self.kv_heads), dtype=torch.float32,
+                              device=self.device)
+        self.scores = backing.permute(0, 2, 1)
+        self.entries = {}
+        self.verify = os.environ.get("GSTAR_EVICT_VERIFY") == "1"
+        self.score_mode = os.environ.get("GSTAR_EVICT_SCORE", "queue")
+        if self.score_mode not in ("queue", "eager"):
+            raise ValueError("GSTAR_EVICT_SCORE must be 'queue' or 'eager'")
+        self.queue_cap = int(os.environ.get("GSTAR_EVICT_QUEUE", "64"))
+        if not 1 <= self.queue_cap <= 64:
+            raise ValueError("GSTAR_EVICT_QUEUE must be in 1..64")
+        self.q_heads = None
+        self.qq = self.qnorm = self.qlim = None
+        self.qcount = torch.zeros((len(self.full_layers), n_rows), **i32)
+        self.queued = {}
+        self.row_ids = torch.arange(n_rows, **i32)
+        self.layer_scaling = {}  # full-layer index -> softmax scale of its queued queries
+        self._ws = {}
+        self._status_host = None
+        self._pools = None
+
+    def workspace(self, name, nbytes):
+        """A cached device byte buffer of at least nbytes (grows, never shrinks)."""
+        buf = self._ws.get(name)
+        if buf is None or buf.numel() < nbytes:
+            buf = self._ws[name] = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=self.device)
+        return buf
+
+    def status_host(self):
+        """A pinned host copy target for a boundary's status words (reused)."""
+        if self._status_host is None:
+            self._status_host = torch.zeros(16, dtype=torch.int32, pin_memory=True)
+        return self._status_host
+
+    def ensure_queue(self):
+        """Allocate the score queues once (the decode kernels fix 8 query heads per KV head)."""
+        if self.qq is not None:
+            return
+        n_rows, layers, cap = self.req_to_token.shape[0], len(self.full_layers), self.queue_cap
+        self.q_heads = 8 * self.kv_heads
+        self.qq = torch.zeros((layers, n_rows, cap, self.q_heads, self.dim), dtype=torch.bfloat16, device=self.device)
+        self.qnorm = torch.zeros((layers, n_rows, cap, self.q_heads), dtype=torch.float32, device=self.device)
+        self.qlim = torch.zeros((layers, n_rows, cap), dtype=torch.int32, device=self.device)
+
+    def pool_pointers(self):
+        """Device arrays of the full layers' K and V buffer addresses, and their shared strides."""
+        keys = [self.pool.get_key_buffer(lid) for lid in self.full_layers]
+        values = [self.pool.get_value_buffer(lid) for lid in self.full_layers]
+        signature = tuple(t.data_ptr() for t in keys + values)
+        if self._pools is None or self._pools[0] != signature:
+            ref = keys[0]
+            for t in keys + values:
+                if t.dtype != torch.bfloat16 or t.stride(-1) != 1 or t.stride()[:2] != ref.stride()[:2]:
+                    raise RuntimeError("gstar_evict needs bf16 K/V pools with one shared layout")
+            as_table = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=self.device)
+            self._pools = (signature, as_table(keys), as_table(values), ref.stride(0), ref.stride(1))
+        return self._pools[1:]
+
+    def release_row(self, row):
+        """Forget a row: its entry, policy mode, eviction state and queued decode steps (queued
+        scores must not land on slots the row no longer owns)."""
+        self.entries.pop(row, None)
+        for t in (self.mode, self.frontier, self.count):
+            t[row] = 0
+        self.qcount[:, row] = 0
+        self.queued.pop(row, None)

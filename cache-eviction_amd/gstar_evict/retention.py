@@ -14,38 +14,9 @@ evict nothing write no record), and the boundary removes its victims.
 """
 from __future__ import annotations
 
-import base64
-import gzip
-import json
-from pathlib import Path
-
 import numpy as np
 
-
-def decode_array(obj):
-    """One `{"dtype", "shape", "data"}` envelope as a numpy array."""
-    raw = base64.b64decode(obj["data"])
-    return np.frombuffer(raw, dtype=np.dtype(obj["dtype"])).reshape(obj["shape"]).copy()
-
-
-def _is_array(obj):
-    return isinstance(obj, dict) and set(obj) == {"dtype", "shape", "data"}
-
-
-def decode_arrays(obj):
-    """Every array envelope inside a decoded payload replaced by its numpy array."""
-    if _is_array(obj):
-        return decode_array(obj)
-    if isinstance(obj, dict):
-        return {k: decode_arrays(v) for k, v in obj.items()}
-    if isinstance(obj, list):
-        return [decode_arrays(v) for v in obj]
-    return obj
-
-
-def read_payload(path):
-    """A payload file (`<key>.json.gz`) with its arrays decoded."""
-    return decode_arrays(json.loads(gzip.decompress(Path(path).read_bytes())))
+from .payloads import decode_array, decode_arrays, read as read_payload  # noqa: F401  (reader API)
 
 
 def evicted_per_head(record):
