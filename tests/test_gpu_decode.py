@@ -26,22 +26,28 @@ def fresh_state():
     ge.STATE = None
 
 
+# T:80-90's known answer: row 1 holds 4 compacted slots below frontier 7 and reads req_to_token
+# from 7 up to its length 10; row 2 (length 6) has had no boundary.
+FILL_KNOWN = dict(r2t={1: list(range(101, 111)), 2: list(range(201, 207))}, table={1: [101, 102, 106, 107]},
+                  count={1: 4}, frontier={1: 7}, rows=[1, 2], lens=[10, 6], indptr=[0, 7, 13],
+                  indices=[101, 102, 106, 107, 108, 109, 110, 201, 202, 203, 204, 205, 206])
+
+
 def test_fill_reads_compact_residents_then_tail():
-    """T:80-90 known answer."""
     b = backend()
     st = ge.state(b)
-    st.req_to_token[1, :10] = torch.arange(101, 111, dtype=torch.int32)
-    st.req_to_token[2, :6] = torch.arange(201, 207, dtype=torch.int32)
-    st.table[1, :4] = torch.tensor([101, 102, 106, 107], dtype=torch.int32)
-    st.count[1], st.frontier[1] = 4, 7
-    out = torch.full((32,), -1, dtype=torch.int64, device="cuda")
-    indptr = ge.fill(b, 2, torch.tensor([10, 6], device="cuda"), torch.tensor([1, 2], device="cuda"), out)
-    assert indptr.tolist() == [0, 7, 13]
-    assert out[:13].tolist() == [101, 102, 106, 107, 108, 109, 110, 201, 202, 203, 204, 205, 206]
-    out32 = torch.full((32,), -1, dtype=torch.int32, device="cuda")
-    ge.fill(b, 2, torch.tensor([10, 6], dtype=torch.int32, device="cuda"),
-            torch.tensor([1, 2], dtype=torch.int32, device="cuda"), out32)
-    assert out32[:13].tolist() == out[:13].tolist()
+    case = FILL_KNOWN
+    for row, slots in case["r2t"].items():
+        st.req_to_token[row, :len(slots)] = torch.tensor(slots, dtype=torch.int32)
+    for row, slots in case["table"].items():
+        st.table[row, :len(slots)] = torch.tensor(slots, dtype=torch.int32)
+        st.count[row], st.frontier[row] = case["count"][row], case["frontier"][row]
+    for dtype in (torch.int64, torch.int32):  # index tensors of either width
+        out = torch.full((32,), -1, dtype=dtype, device="cuda")
+        as_dev = lambda v: torch.tensor(v, dtype=dtype, device="cuda")
+        indptr = ge.fill(b, 2, as_dev(case["lens"]), as_dev(case["rows"]), out)
+        assert indptr.tolist() == case["indptr"]
+        assert out[:len(case["indices"])].tolist() == case["indices"]
 
 
 def test_fill_matches_oracle_on_random_rows():
@@ -175,14 +181,14 @@ def test_after_decode_rebuilds_normaliser_from_split_lse(mode):
     st.mode[:] = mode
     ge.after_decode(b, q.reshape(3, -1), layer(1), SimpleNamespace(
         out_cache_loc=torch.zeros(3, dtype=torch.int64, device="cuda"), req_pool_indices=rows), sinks)
-    expected = torch.zeros_like(st.scores)
+    expected = np.zeros(tuple(st.scores.shape[1:]))
     for i in range(3):
-        slots = perm[indptr[i]:indptr[i + 1]].long()
-        k = b.token_to_kv_pool.get_key_buffer(1)[slots].float().repeat_interleave(8, 1)
-        logits = torch.einsum("hd,khd->hk", q[i].float(), k) * 0.125
-        p = torch.softmax(torch.cat((logits, sinks.float()[:, None]), -1), -1)[:, :-1].view(8, 8, -1)
-        expected[0][:, slots] += p.sum(1) if mode == 1 else p.amax(1)
-    torch.testing.assert_close(st.scores, expected, rtol=2e-3, atol=1e-6)
+        rows_keys = perm[indptr[i]:indptr[i + 1]].cpu().numpy()
+        qn = q[i].float().cpu().numpy()
+        _, norm = O.decode_attention(qn, keys, keys, rows_keys, sinks.float().cpu().numpy(), 0.125)
+        O.decode_scores_into(expected, qn, keys, rows_keys, norm, 0.125, mode)
+    torch.testing.assert_close(st.scores[0].cpu(), torch.tensor(expected, dtype=torch.float32), rtol=2e-3, atol=1e-6)
+    assert float(st.scores[1:].abs().sum()) == 0.0
 
 
 def test_rows_without_a_policy_get_no_scores_and_sliding_layers_are_skipped():
