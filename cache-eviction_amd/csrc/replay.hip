@@ -1,0 +1,343 @@
+// Static replay's layer difference (R:520-546): for every query of a prefill chunk, the
+// relative L2 distance between the first full layer's attention output over the unevicted keys
+// (a) and over each KV head's survivors (b), both with the sink in the normaliser:
+//   error[i] = |b_i - a_i| / max(|a_i|, 1e-12), norms over all query heads x 64 dims.
+//
+// One kernel computes one of the two outputs; it runs twice per chunk (all keys, then the
+// survivors) and a small kernel reduces the two to the per-query errors.
+//
+// Output kernel, per workgroup: one KV head and 32 queries (8 waves x 2 row-blocks). A
+// row-block is 16 MFMA columns, (query, head) pairs: queries 2*rb and 2*rb + 1, the KV head's
+// 8 query heads each. Per 64-key tile:
+//   S^T = K . Q^T            4 key-blocks x 2 dim halves (v_mfma_f32_16x16x32_bf16)
+//   online softmax           one running reference per column, moved lazily (by > 2^8)
+//   O^T += V^T . P^T         V transposed through LDS (ds_read_b64_tr_b16); P split into
+//                            bf16 hi + lo parts, so products carry ~16 mantissa bits of P
+// K and V tiles go through LDS, double-buffered (threads 0-255 stage K, 256-511 stage V).
+//
+// Key columns: column c < n_retained is key row retained[g][c]; column c >= n_retained is key
+// row tail0 + (c - n_retained). Query i sees columns <= prefix_len + i. With n_retained = 0 and
+// tail0 = 0 that is plain causal attention over rows 0..prefix_len + i.
+#include <type_traits>
+
+#include "common.hpp"
+#include "host.hpp"
+
+namespace gse {
+
+namespace rp {
+constexpr int D = 64;
+constexpr int GROUP = 8;
+constexpr int RB = 2;                    // row-blocks per wave
+constexpr int WAVES = 8;
+constexpr int QB = 2 * RB * WAVES;       // queries per workgroup (32)
+constexpr int KT = 64;                   // keys per tile
+constexpr int KROW = D + 8;              // padded bf16 row of a staged K row
+constexpr int VROW = D + 16;             // padded bf16 row of a staged V row (transposed reads)
+constexpr float RESCALE = 8.f;
+}  // namespace rp
+
+struct ReplayArgs {
+  const uint16_t* q;
+  int64_t q_st, q_sh, count;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t kv_ss, kv_sh, rows;  // rows: key rows of k and v (out-of-range rows read row 0)
+  const int32_t* retained;     // [kv_heads][ret_sg] key rows of the first n_retained columns
+  int64_t ret_sg, n_retained, tail0;
+  int64_t prefix_len;
+  const void* sinks;
+  int sinks_dtype;
+  int q_heads, kv_heads;
+  float scale2;
+  float* out;  // [count, q_heads, 64] fp32
+};
+
+// One 64-key tile for the wave's row-blocks. s[kb][r] is S^T[key 16*kb + 4*grp + r][column].
+// MASKED: key column t0 + 16*kb + 4*grp + r is dead for column `col`'s query when
+// rel + 16*kb + r > 2*rb + col/8, with rel = t0 + 4*grp - (prefix_len + first query of the wave).
+template <bool MASKED>
+GSE_DEVICE void replay_tile(const bf16x8_t (&qa)[rp::RB][2], const bf16x8_t (&kb0)[4], const bf16x8_t (&kb1)[4],
+                            const bf16x8_t (&va)[4][2], float (&ref)[rp::RB], float (&lsum)[rp::RB],
+                            f32x4_t (&o)[rp::RB][4], float scale2, int64_t rel, int col) {
+  using namespace rp;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    f32x4_t s[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      s[kb] = mfma16x16x32(kb0[kb], qa[rb][0], f32x4_t{0.f, 0.f, 0.f, 0.f});
+      s[kb] = mfma16x16x32(kb1[kb], qa[rb][1], s[kb]);
+    }
+    if (MASKED) {
+      const int64_t qrel = 2 * rb + (col >> 3);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (rel + 16 * kb + r > qrel) s[kb][r] = -INFINITY;
+    }
+    float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(s[2][0], s[2][1]), fmaxf(s[2][2], s[2][3])),
+                             fmaxf(fmaxf(s[3][0], s[3][1]), fmaxf(s[3][2], s[3][3]))));
+    tmax = xor32_max(xor16_max(tmax)) * scale2;  // the column's maximum over the tile (scale > 0)
+    // Wave-uniform: the rescale runs only in tiles where some column's maximum moved by > 2^8.
+    if (__builtin_amdgcn_ballot_w64(tmax > ref[rb] + RESCALE)) {
+      const float nr = tmax > ref[rb] + RESCALE ? tmax : ref[rb];
+      const float corr = fast_exp2(ref[rb] - nr);
+      ref[rb] = nr;
+      lsum[rb] *= corr;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[rb][j] = o[rb][j] * corr;
+    }
+    float p[4][4];
+    float ps = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[kb][r] = fast_exp2(fmaf(s[kb][r], scale2, -ref[rb]));
+        ps += p[kb][r];
+      }
+    lsum[rb] += ps;
+    // P^T operands: half h covers key-blocks 2h and 2h + 1; k-element e maps to key-block
+    // 2h + e/4, key 4*grp + e%4 (the layout of va). hi = bf16(p), lo = bf16(p - hi).
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint4 hi, lo;
+      float rem[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = p[2 * h + e / 4][e % 4];
+        rem[e] = x;
+      }
+      hi.x = pack_bf16x2(rem[0], rem[1]);
+      hi.y = pack_bf16x2(rem[2], rem[3]);
+      hi.z = pack_bf16x2(rem[4], rem[5]);
+      hi.w = pack_bf16x2(rem[6], rem[7]);
+      const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w = hw[e / 2];
+        const float part = __uint_as_float(e % 2 ? (w & 0xffff0000u) : (w << 16));
+        rem[e] -= part;
+      }
+      lo.x = pack_bf16x2(rem[0], rem[1]);
+      lo.y = pack_bf16x2(rem[2], rem[3]);
+      lo.z = pack_bf16x2(rem[4], rem[5]);
+      lo.w = pack_bf16x2(rem[6], rem[7]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[rb][j] = mfma16x16x32(va[j][h], as_bf16x8(hi), o[rb][j]);
+        o[rb][j] = mfma16x16x32(va[j][h], as_bf16x8(lo), o[rb][j]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+__global__ __launch_bounds__(64 * rp::WAVES) void replay_output_kernel(ReplayArgs a) {
+  using namespace rp;
+  __shared__ __attribute__((aligned(16))) uint16_t ktile[2][KT * KROW];
+  __shared__ __attribute__((aligned(16))) uint16_t vtile[2][KT * VROW];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  // Heaviest query blocks first: linear block i -> KV head i % kv_heads, query block from the end.
+  const int64_t nqb = (a.count + QB - 1) / QB;
+  const int g = blockIdx.x % a.kv_heads;
+  const int64_t qb0 = (nqb - 1 - int64_t(blockIdx.x / a.kv_heads)) * QB;
+  const int64_t i0 = qb0 + 2 * RB * wave;
+  const int64_t last_q = (qb0 + QB < a.count ? qb0 + QB : a.count) - 1;
+  const int64_t kend = a.prefix_len + last_q + 1;  // columns any query of the workgroup sees
+  const bool wave_live = i0 < a.count;
+  const int64_t wave_kend = a.prefix_len + (i0 + 2 * RB - 1 < a.count ? i0 + 2 * RB - 1 : a.count - 1) + 1;
+
+  // Q^T fragments: column col of row-block rb is query i0 + 2*rb + col/8, head g*8 + col%8;
+  // lane group grp supplies dims [16*grp, 16*grp + 16) as two 8-dim MFMA halves.
+  bf16x8_t qa[RB][2];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int64_t qi = i0 + 2 * rb + col / 8;
+    qa[rb][0] = bf16x8_t{};
+    qa[rb][1] = bf16x8_t{};
+    if (qi < a.count) {
+      const uint16_t* qp = a.q + qi * a.q_st + int64_t(g * GROUP + col % 8) * a.q_sh + 16 * grp;
+      qa[rb][0] = as_bf16x8(*reinterpret_cast<const uint4*>(qp));
+      qa[rb][1] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 8));
+    }
+  }
+  float ref[RB], lsum[RB];
+  f32x4_t o[RB][4];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    ref[rb] = -1e30f;  // finite: the first tile's rescale multiplies zeros by 2^(-huge) = 0
+    lsum[rb] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[rb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Staging: thread t holds row (t/4) % 64, dims [16*(t%4), +16) of K (t < 256) or V.
+  const bool stage_v = threadIdx.x >= 256;
+  const int lk = (threadIdx.x >> 2) & 63, lp = threadIdx.x & 3;
+  const uint16_t* src = stage_v ? a.v : a.k;
+  auto load_tile = [&](int64_t t0, uint4& x0, uint4& x1) {
+    const int64_t c = t0 + lk;
+    int64_t row = 0;
+    if (c < kend) row = c < a.n_retained ? int64_t(a.retained[g * a.ret_sg + c]) : a.tail0 + (c - a.n_retained);
+    if (row < 0 || row >= a.rows) row = 0;
+    const auto p = as_global(src) + row * a.kv_ss + int64_t(g) * a.kv_sh + 16 * lp;
+    x0 = gload16(p);
+    x1 = gload16(p + 8);
+  };
+  auto store_tile = [&](int buf, uint4 x0, uint4 x1) {
+    uint16_t* dst = stage_v ? &vtile[buf][lk * VROW + 16 * lp] : &ktile[buf][lk * KROW + 16 * lp];
+    *reinterpret_cast<uint4*>(dst) = x0;
+    *reinterpret_cast<uint4*>(dst + 8) = x1;
+  };
+  const int ntiles = int((kend + KT - 1) / KT);
+  uint4 x0 = {}, x1 = {};
+  load_tile(0, x0, x1);
+  store_tile(0, x0, x1);
+  __syncthreads();
+
+#pragma unroll 1
+  for (int ti = 0; ti < ntiles; ++ti) {
+    const int64_t t0 = int64_t(ti) * KT;
+    if (ti + 1 < ntiles) load_tile(t0 + KT, x0, x1);  // in flight during this tile's compute
+    if (wave_live && t0 < wave_kend) {
+      const uint16_t* kt = ktile[ti & 1];
+      bf16x8_t kb0[4], kb1[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint16_t* kr = kt + (16 * kb + col) * KROW + 16 * grp;
+        kb0[kb] = as_bf16x8(*reinterpret_cast<const uint4*>(kr));
+        kb1[kb] = as_bf16x8(*reinterpret_cast<const uint4*>(kr + 8));
+      }
+      // V^T fragments of dim block j, half h: lane (dim 16*j + lane%16, group grp) holds keys
+      // 32*h + 4*grp + e (e < 4) and 32*h + 16 + 4*grp + (e - 4).
+      bf16x8_t va[4][2];
+      const uint16_t* vr = vtile[ti & 1] + (4 * grp + (col >> 2)) * VROW + 4 * (col & 3);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        va[j][0] = join_bf16x8(ds_read_tr16(vr + 16 * j), ds_read_tr16(vr + 16 * VROW + 16 * j));
+        va[j][1] = join_bf16x8(ds_read_tr16(vr + 32 * VROW + 16 * j), ds_read_tr16(vr + 48 * VROW + 16 * j));
+      }
+      const int64_t qpos0 = a.prefix_len + i0;
+      if (t0 + KT - 1 > qpos0)
+        replay_tile<true>(qa, kb0, kb1, va, ref, lsum, o, a.scale2, t0 + 4 * grp - qpos0, col);
+      else
+        replay_tile<false>(qa, kb0, kb1, va, ref, lsum, o, a.scale2, 0, col);
+    }
+    if (ti + 1 < ntiles) store_tile((ti + 1) & 1, x0, x1);
+    __syncthreads();
+  }
+
+  if (!wave_live) return;
+  const int hq = g * GROUP + (col & 7);
+  const float sink2 = load_float_dyn(a.sinks, a.sinks_dtype, hq) * kLog2e;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int64_t qi = i0 + 2 * rb + (col >> 3);
+    const float l = xor32_sum(xor16_sum(lsum[rb]));  // the column's sum over the four lane groups
+    const float m = fmaxf(ref[rb], sink2);
+    const float keep = fast_exp2(ref[rb] - m);
+    const float inv = keep / (l * keep + fast_exp2(sink2 - m));
+    if (qi < a.count) {
+      float* op = a.out + (qi * a.q_heads + hq) * D + 4 * grp;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 w = {o[rb][j][0] * inv, o[rb][j][1] * inv, o[rb][j][2] * inv, o[rb][j][3] * inv};
+        *reinterpret_cast<float4*>(op + 16 * j) = w;
+      }
+    }
+  }
+}
+
+// error[i] = |b_i - a_i| / max(|a_i|, 1e-12) over `width` floats per query; one wave per query.
+__global__ __launch_bounds__(256) void replay_error_kernel(const float* a, const float* b, int64_t count, int width,
+                                                         float* error) {
+  const int64_t i = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= count) return;
+  const float4* pa = reinterpret_cast<const float4*>(a + i * width);
+  const float4* pb = reinterpret_cast<const float4*>(b + i * width);
+  float dd = 0.f, aa = 0.f;
+  for (int t = lane; t < width / 4; t += kWave) {
+    const float4 x = pa[t], y = pb[t];
+    const float d0 = y.x - x.x, d1 = y.y - x.y, d2 = y.z - x.z, d3 = y.w - x.w;
+    dd += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    aa += (x.x * x.x + x.y * x.y) + (x.z * x.z + x.w * x.w);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    dd += __shfl_xor(dd, off, kWave);
+    aa += __shfl_xor(aa, off, kWave);
+  }
+  if (lane == 0) error[i] = sqrtf(dd) / fmaxf(sqrtf(aa), 1e-12f);
+}
+
+}  // namespace gse
+
+using namespace gse;
+
+extern "C" int64_t gse_replay_workspace_bytes(int64_t count, int q_heads) {
+  return 2 * ((count * q_heads * rp::D * 4 + 255) / 256) * 256;
+}
+
+extern "C" int gse_replay_layer_difference(const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t count,
+                                           const void* k_shadow, const void* v_shadow, int64_t kv_stride_s,
+                                           int64_t kv_stride_h, int64_t shadow_rows, int64_t start,
+                                           const int32_t* retained, int64_t retained_stride_g,
+                                           int64_t retained_count, int64_t frontier, const void* sinks,
+                                           int sinks_dtype, int q_heads, int kv_heads, int head_dim, float sm_scale,
+                                           float* error, void* workspace, int64_t workspace_bytes,
+                                           gse_stream_t stream) {
+  if (head_dim != rp::D || kv_heads < 1 || q_heads != rp::GROUP * kv_heads)
+    return gse_fail(GSE_ESHAPE, "replay: need head_dim 64 and q_heads == 8 * kv_heads");
+  if (count < 0 || start < 0 || retained_count < 0 || frontier < 0)
+    return gse_fail(GSE_EINVAL, "replay: negative count, start, retained_count or frontier");
+  if (count == 0) return GSE_OK;
+  if (retained_count > 0 && frontier > start)
+    return gse_fail(GSE_EINVAL, "replay: the chunk must start at or after the frontier");
+  if (shadow_rows < start + count) return gse_fail(GSE_EINVAL, "replay: the shadow must hold start + count rows");
+  if (q_stride_t % 8 || q_stride_h % 8 || kv_stride_s % 8 || kv_stride_h % 8)
+    return gse_fail(GSE_EINVAL, "replay: strides must be multiples of 8 elements");
+  if (!q || !k_shadow || !v_shadow || !sinks || !error || (retained_count && !retained))
+    return gse_fail(GSE_EINVAL, "replay: null pointer");
+  if (retained_count && retained_stride_g < retained_count)
+    return gse_fail(GSE_EINVAL, "replay: retained rows overlap");
+  if (workspace_bytes < gse_replay_workspace_bytes(count, q_heads))
+    return gse_fail(GSE_EWORKSPACE, "replay: workspace too small");
+  const int64_t blocks = (count + rp::QB - 1) / rp::QB * kv_heads;
+  if (blocks >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "replay: chunk too large");
+  float* full = static_cast<float*>(workspace);
+  float* kept = full + gse_replay_workspace_bytes(count, q_heads) / 8;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid{static_cast<uint32_t>(blocks)};
+  // a: every key up to the query (columns are positions).
+  ReplayArgs a = {static_cast<const uint16_t*>(q), q_stride_t, q_stride_h, count,
+                  static_cast<const uint16_t*>(k_shadow), static_cast<const uint16_t*>(v_shadow), kv_stride_s,
+                  kv_stride_h, shadow_rows, nullptr, 0, 0, 0, start, sinks, sinks_dtype, q_heads, kv_heads,
+                  sm_scale * kLog2e, full};
+  hipLaunchKernelGGL(replay_output_kernel, grid, dim3(64 * rp::WAVES), 0, s, a);
+  if (int rc = gse_launch_check("replay full output")) return rc;
+  const float* b = full;  // nothing evicted yet: the outputs coincide and every error is 0
+  if (retained_count > 0) {
+    // b: each head's retained positions, then positions frontier .. start + count - 1.
+    ReplayArgs e = a;
+    e.retained = retained;
+    e.ret_sg = retained_stride_g;
+    e.n_retained = retained_count;
+    e.tail0 = frontier;
+    e.prefix_len = retained_count + start - frontier;
+    e.out = kept;
+    hipLaunchKernelGGL(replay_output_kernel, grid, dim3(64 * rp::WAVES), 0, s, e);
+    if (int rc = gse_launch_check("replay survivors' output")) return rc;
+    b = kept;
+  }
+  const dim3 egrid{static_cast<uint32_t>((count + 3) / 4)};
+  hipLaunchKernelGGL(replay_error_kernel, egrid, dim3(256), 0, s, full, b, count, q_heads * rp::D, error);
+  return gse_launch_check("replay error");
+}

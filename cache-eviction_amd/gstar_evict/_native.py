@@ -49,6 +49,9 @@ SIGNATURES = {
                                 _f, _p, _l, _p]),
     "gse_diagnose_chunk": (_i, [_p, _l, _l, _l, _p, _l, _l, _p, _i, _l, _l, _p, _i, _p, _p, _l, _l, _p, _i, _l,
                                 _l, _p, _l, _f, _i, _i, _i, _f, _p, _l, _p]),
+    "gse_replay_workspace_bytes": (_l, [_l, _i]),
+    "gse_replay_layer_difference": (_i, [_p, _l, _l, _l, _p, _p, _l, _l, _l, _l, _p, _l, _l, _l, _p, _i, _i, _i,
+                                         _i, _f, _p, _p, _l, _p]),
 }
 
 _lock = threading.Lock()

@@ -286,6 +286,30 @@ int gse_diagnose_chunk(const void* q, int64_t q_stride_t, int64_t q_stride_h, in
                        float lost_scale, int q_heads, int kv_heads, int head_dim, float sm_scale,
                        void* workspace, int64_t workspace_bytes, gse_stream_t stream);
 
+/*
+ * replay_layer_difference — static replay's per-query error of the first full
+ * layer for one prefill chunk (R:520-546, `_replay_layer_difference`):
+ *   a_i = attention of query start+i over positions 0..start+i (all unevicted keys)
+ *   b_i = the same over each KV head's survivors: retained[g][0..retained_count)
+ *         then positions frontier..start+i
+ *   error[i] = |b_i - a_i| / max(|a_i|, 1e-12)   (norm over q_heads x head_dim)
+ * Both with the sink in the normaliser. k_shadow / v_shadow hold the layer's
+ * unevicted keys and values by position ([shadow_rows, kv_heads, head_dim]
+ * bf16, shadow_rows >= start + count); retained positions (int32, rows
+ * retained_stride_g apart) lie below frontier <= start. retained_count = 0
+ * (nothing evicted yet) gives error 0. head_dim = 64, q_heads = 8 * kv_heads.
+ * MFMA 16x16x32 bf16 tiles with a single-pass online softmax; probabilities
+ * enter the value product as bf16 hi + lo parts.
+ */
+int64_t gse_replay_workspace_bytes(int64_t count, int q_heads);
+int gse_replay_layer_difference(const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t count,
+                                const void* k_shadow, const void* v_shadow, int64_t kv_stride_s,
+                                int64_t kv_stride_h, int64_t shadow_rows, int64_t start, const int32_t* retained,
+                                int64_t retained_stride_g, int64_t retained_count, int64_t frontier,
+                                const void* sinks, int sinks_dtype, int q_heads, int kv_heads, int head_dim,
+                                float sm_scale, float* error, void* workspace, int64_t workspace_bytes,
+                                gse_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
