@@ -56,6 +56,9 @@ def parse(argv=None):
     p.add_argument("--prefill", action="store_true",
                    help="time the chunked-prefill score tiles instead: 12 layers, 79,720-token prompt in "
                         "8192-token chunks, prefix capped at the 28,672-token budget (MFMA roofline)")
+    p.add_argument("--replay", action="store_true",
+                   help="time static replay's layer difference instead: first full layer, 79,720-token prompt "
+                        "in 2048-token chunks, 2048 positions retained per KV head (MFMA roofline)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="only run a plain device copy of this many MiB (5 launches): the byte-counter "
                         "calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE runs")
@@ -448,6 +451,73 @@ def prefill_bench(args, torch, ge):
     }
 
 
+def replay_bench(args, torch, ge):
+    """Static replay's layer difference over a 79,720-token prompt in 2048-token chunks with
+    2048 positions retained per KV head after each boundary: per chunk, the first full layer's
+    output over every earlier key and over each head's survivors, then the per-query relative
+    error. Algorithmic work = 4 * 64 dims flop per (query head, visible key) pair and output
+    (QK^T and PV, one each); the kernel issues PV twice (probabilities as bf16 hi + lo)."""
+    prompt, chunk, budget = 79720, 2048, 2048
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    k = torch.randn((prompt, HKV, D), device="cuda", generator=g)
+    u = torch.randn((HKV, D), device="cuda", generator=g)
+    heavy = torch.rand((prompt, HKV), device="cuda", generator=g) < 0.02
+    k = torch.where(heavy[..., None], 4 * k.norm(dim=-1, keepdim=True) * (u / u.norm(dim=-1, keepdim=True)), k)
+    sk = k.to(torch.bfloat16)
+    sv = torch.randn((prompt, HKV, D), device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn((chunk, HQ, D), device="cuda", generator=g).to(torch.bfloat16)
+    sinks = torch.randn(HQ, device="cuda", generator=g)
+    layer = SimpleNamespace(tp_q_head_num=HQ, tp_k_head_num=HKV, qk_head_dim=D, scaling=D ** -0.5)
+    pool = SimpleNamespace(layers_mapping={0: (0, False)}, get_key_buffer=lambda l: sk, get_value_buffer=lambda l: sv)
+    backend = SimpleNamespace(token_to_kv_pool=pool, max_kv_splits=16,
+                              req_to_token_pool=SimpleNamespace(req_to_token=torch.zeros((2, 64), dtype=torch.int32,
+                                                                                         device="cuda")),
+                              kv_indptr=torch.zeros(3, dtype=torch.int32, device="cuda"))
+    ge.STATE = None
+    st = ge.state(backend)
+    plan = []  # (start, count, entry): the boundary at each multiple of 2048 above the budget evicts
+    for start in range(0, prompt, chunk):
+        count = min(chunk, prompt - start)
+        entry = {"shadow_k": sk, "shadow_v": sv, "frontier": 0, "count": 0, "layer_error": []}
+        if start > budget:
+            pos = torch.rand((HKV, start), device="cuda", generator=g).argsort(-1)[:, :budget].sort(-1).values
+            entry.update(frontier=start, count=budget, pos=pos.to(torch.int32)[None])
+        plan.append((start, count, entry))
+
+    def run():
+        for start, count, entry in plan:
+            entry["layer_error"].clear()
+            ge._replay_layer_difference(st, entry, q[:count], layer, sinks, start)
+
+    run()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = max(1, min(args.steps, 5))
+    t0.record()
+    for _ in range(reps):
+        run()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    pairs = sum(start * count + count * (count + 1) // 2 for start, count, _ in plan)
+    kept_pairs = sum(budget * count + count * (count + 1) // 2 for start, count, e in plan if e["count"])
+    flop = (pairs + kept_pairs) * HQ * 4 * D
+    tflops = flop / (ms * 1e-3) / 1e12
+    return {
+        "metric": "replay layer difference, TFLOP/s (QK^T + PV per output) and % of bf16 MFMA peak",
+        "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "gpt-oss-20b first full layer, 79,720-token prompt in 2048-token chunks, 2048 "
+                               "positions retained per KV head, 2% heavy-hitter keys",
+                   "causal_pairs": pairs, "retained_pairs": kept_pairs},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "issued_frac": round(1.5 * tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "exp2_T_per_s": round((pairs + kept_pairs) * HQ / (ms * 1e-3) / 1e12, 2),
+    }
+
+
 def workload_name(args):
     k = lambda n: f"{n // 1024}K" if n % 1024 == 0 else str(n)
     scored = args.budget - args.prefix - args.recent
@@ -476,6 +546,9 @@ def main():
         return
     if args.prefill:
         print(json.dumps(prefill_bench(args, torch, ge)), flush=True)
+        return
+    if args.replay:
+        print(json.dumps(replay_bench(args, torch, ge)), flush=True)
         return
     w = Workload(args, torch, ge)
     for _ in range(args.warmup):

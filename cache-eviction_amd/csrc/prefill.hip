@@ -35,6 +35,7 @@ constexpr int KT = 64;          // keys per tile (4 key-blocks of 16)
 constexpr int KROW = D + 8;     // padded bf16 row of a staged key
 constexpr int RING = 16;        // tiles of column sums held before they are added to the scores
 constexpr float RESCALE = 8.f;  // a row's reference maximum moves when a logit exceeds it by 2^8
+constexpr float kRescaleSum = 256.f;  // 2^RESCALE
 }  // namespace pf
 
 struct PrefillArgs {
@@ -92,31 +93,44 @@ GSE_DEVICE void prefill_tile(const bf16x8_t (&qa)[RB][2], const bf16x8_t (&kb0)[
           for (int r = 0; r < 4; ++r) d[kb][r] = -INFINITY;
     }
     if (PASS == 1) {
-      float tmax[4];
-      bool need = false;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        tmax[r] = fmaxf(fmaxf(d[0][r], d[1][r]), fmaxf(d[2][r], d[3][r])) * scale2;
-        need |= tmax[r] > ref[rb][r] + RESCALE;
-      }
-      // A wave-uniform branch, so the rescale's exponentials run only in the (rare) tiles
-      // where some row's maximum moved.
-      if (__builtin_amdgcn_ballot_w64(need)) {
+      // Row sums of 2^(x - ref) over this lane's four keys. A sum past 2^RESCALE may hide a
+      // key past it: then (rarely, wave-uniform) the exact row maxima decide the lazy rescale
+      // and the sums are recomputed for the moved references.
+      float ts[4];
+      auto expo = [&]() {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float nr = tmax[r] > ref[rb][r] + RESCALE ? tmax[r] : ref[rb][r];
-          sum[rb][r] *= fast_exp2(ref[rb][r] - nr);
-          ref[rb][r] = nr;
+          const float e0 = fast_exp2(fmaf(d[0][r], scale2, -ref[rb][r]));
+          const float e1 = fast_exp2(fmaf(d[1][r], scale2, -ref[rb][r]));
+          const float e2 = fast_exp2(fmaf(d[2][r], scale2, -ref[rb][r]));
+          const float e3 = fast_exp2(fmaf(d[3][r], scale2, -ref[rb][r]));
+          ts[r] = (e0 + e1) + (e2 + e3);
+        }
+      };
+      expo();
+      bool big = false;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) big |= !(ts[r] <= kRescaleSum);
+      if (__builtin_amdgcn_ballot_w64(big)) {
+        float tmax[4];
+        bool need = false;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          tmax[r] = fmaxf(fmaxf(d[0][r], d[1][r]), fmaxf(d[2][r], d[3][r])) * scale2;
+          need |= tmax[r] > ref[rb][r] + RESCALE;
+        }
+        if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float nr = tmax[r] > ref[rb][r] + RESCALE ? tmax[r] : ref[rb][r];
+            sum[rb][r] *= fast_exp2(ref[rb][r] - nr);
+            ref[rb][r] = nr;
+          }
+          expo();
         }
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e0 = fast_exp2(fmaf(d[0][r], scale2, -ref[rb][r]));
-        const float e1 = fast_exp2(fmaf(d[1][r], scale2, -ref[rb][r]));
-        const float e2 = fast_exp2(fmaf(d[2][r], scale2, -ref[rb][r]));
-        const float e3 = fast_exp2(fmaf(d[3][r], scale2, -ref[rb][r]));
-        sum[rb][r] += (e0 + e1) + (e2 + e3);
-      }
+      for (int r = 0; r < 4; ++r) sum[rb][r] += ts[r];
     } else {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {

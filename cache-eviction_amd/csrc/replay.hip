@@ -35,6 +35,7 @@ constexpr int KT = 64;                   // keys per tile
 constexpr int KROW = D + 8;              // padded bf16 row of a staged K row
 constexpr int VROW = D + 16;             // padded bf16 row of a staged V row (transposed reads)
 constexpr float RESCALE = 8.f;
+constexpr float kRescaleSum = 256.f;  // 2^RESCALE
 }  // namespace rp
 
 struct ReplayArgs {
@@ -77,63 +78,57 @@ GSE_DEVICE void replay_tile(const bf16x8_t (&qa)[rp::RB][2], const bf16x8_t (&kb
         for (int r = 0; r < 4; ++r)
           if (rel + 16 * kb + r > qrel) s[kb][r] = -INFINITY;
     }
-    float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-    tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(s[2][0], s[2][1]), fmaxf(s[2][2], s[2][3])),
-                             fmaxf(fmaxf(s[3][0], s[3][1]), fmaxf(s[3][2], s[3][3]))));
-    tmax = xor32_max(xor16_max(tmax)) * scale2;  // the column's maximum over the tile (scale > 0)
-    // Wave-uniform: the rescale runs only in tiles where some column's maximum moved by > 2^8.
-    if (__builtin_amdgcn_ballot_w64(tmax > ref[rb] + RESCALE)) {
-      const float nr = tmax > ref[rb] + RESCALE ? tmax : ref[rb];
-      const float corr = fast_exp2(ref[rb] - nr);
-      ref[rb] = nr;
-      lsum[rb] *= corr;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o[rb][j] = o[rb][j] * corr;
-    }
+    // p = 2^(x*scale2 - ref). A lane whose 16 values sum past 2^RESCALE may hold one past it:
+    // then (rarely, wave-uniform) the exact column maxima decide the lazy rescale, and p is
+    // recomputed for the new references.
     float p[4][4];
-    float ps = 0.f;
+    auto expo = [&]() {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[kb][r] = fast_exp2(fmaf(s[kb][r], scale2, -ref[rb]));
-        ps += p[kb][r];
+        for (int r = 0; r < 4; ++r) p[kb][r] = fast_exp2(fmaf(s[kb][r], scale2, -ref[rb]));
+      const float a0 = (p[0][0] + p[0][1]) + (p[0][2] + p[0][3]), a1 = (p[1][0] + p[1][1]) + (p[1][2] + p[1][3]);
+      const float a2 = (p[2][0] + p[2][1]) + (p[2][2] + p[2][3]), a3 = (p[3][0] + p[3][1]) + (p[3][2] + p[3][3]);
+      return (a0 + a1) + (a2 + a3);
+    };
+    float ps = expo();
+    if (__builtin_amdgcn_ballot_w64(!(ps <= kRescaleSum))) {
+      float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                         fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+      tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(s[2][0], s[2][1]), fmaxf(s[2][2], s[2][3])),
+                               fmaxf(fmaxf(s[3][0], s[3][1]), fmaxf(s[3][2], s[3][3]))));
+      tmax = xor32_max(xor16_max(tmax)) * scale2;  // the column's maximum over the tile (scale > 0)
+      if (__builtin_amdgcn_ballot_w64(tmax > ref[rb] + RESCALE)) {
+        const float nr = tmax > ref[rb] + RESCALE ? tmax : ref[rb];
+        const float corr = fast_exp2(ref[rb] - nr);
+        ref[rb] = nr;
+        lsum[rb] *= corr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[rb][j] = o[rb][j] * corr;
+        ps = expo();
       }
+    }
     lsum[rb] += ps;
     // P^T operands: half h covers key-blocks 2h and 2h + 1; k-element e maps to key-block
-    // 2h + e/4, key 4*grp + e%4 (the layout of va). hi = bf16(p), lo = bf16(p - hi).
+    // 2h + e/4, key 4*grp + e%4 (the layout of va). hi = p truncated to bf16 (v_perm of the
+    // upper halves), lo = bf16(p - hi).
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      uint4 hi, lo;
-      float rem[8];
+      uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = p[2 * h + e / 4][e % 4];
-        rem[e] = x;
+      for (int e = 0; e < 8; e += 2) {
+        const float x0 = p[2 * h + e / 4][e % 4], x1 = p[2 * h + e / 4][e % 4 + 1];
+        const uint32_t b0 = __float_as_uint(x0), b1 = __float_as_uint(x1);
+        hw[e / 2] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+        lw[e / 2] = pack_bf16x2(x0 - __uint_as_float(b0 & 0xffff0000u), x1 - __uint_as_float(b1 & 0xffff0000u));
       }
-      hi.x = pack_bf16x2(rem[0], rem[1]);
-      hi.y = pack_bf16x2(rem[2], rem[3]);
-      hi.z = pack_bf16x2(rem[4], rem[5]);
-      hi.w = pack_bf16x2(rem[6], rem[7]);
-      const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t w = hw[e / 2];
-        const float part = __uint_as_float(e % 2 ? (w & 0xffff0000u) : (w << 16));
-        rem[e] -= part;
-      }
-      lo.x = pack_bf16x2(rem[0], rem[1]);
-      lo.y = pack_bf16x2(rem[2], rem[3]);
-      lo.z = pack_bf16x2(rem[4], rem[5]);
-      lo.w = pack_bf16x2(rem[6], rem[7]);
+      const uint4 hi = {hw[0], hw[1], hw[2], hw[3]}, lo = {lw[0], lw[1], lw[2], lw[3]};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         o[rb][j] = mfma16x16x32(va[j][h], as_bf16x8(hi), o[rb][j]);
         o[rb][j] = mfma16x16x32(va[j][h], as_bf16x8(lo), o[rb][j]);
       }
     }
-    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
