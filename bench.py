@@ -216,7 +216,20 @@ class Workload:
         self.step_index = 0
         self.bytes = 0.0
         self.boundaries = 0
+        self.started = []  # (sequence, n) of the boundaries queued in timed steps
+        self.unaccounted = None  # sequence lengths of the last step, until its boundaries finish
         self.resident_hist = []
+
+    def account_boundaries(self):
+        """Add the algorithmic bytes of every finished boundary queued in a timed step."""
+        a = self.args
+        for i, n in self.started:
+            ev = next(ev for ev in self.entries[i]["events"] if ev["boundary"] == n)
+            if "freed" in ev:
+                width = ev["after"] - (a.prefix + a.recent)
+                self.bytes += boundary_bytes(ev["before"], max(width, 0), ev["after"], ev["freed"], a.layers)
+                self.boundaries += 1
+        self.started = []
 
     def resident(self, i):
         e = self.entries[i]
@@ -224,17 +237,17 @@ class Workload:
 
     def step(self, account=True):
         torch, ge, st, a = self.torch, self.ge, self.st, self.args
-        # Boundaries before the new query (R:692-710): n tokens are cached.
+        # The decode hook's order (on_decode, R:692-710): finish the boundaries the previous step
+        # queued, then queue the boundaries due before the new query (n tokens are cached), at
+        # this workload's interval.
+        ge.finish_boundaries(st)
+        self.account_decode()
         for i, e in enumerate(self.entries):
             n = self.lens[i]
             if n % a.interval == 0 and n > e["last_boundary"]:
-                before = e["count"] + n - e["frontier"]
-                ge._boundary(st, i + 1, e, n, n - 256, self.alloc)
-                ev = e["events"][-1]
-                if account and "freed" in ev:
-                    width = ev["after"] - (a.prefix + a.recent)
-                    self.bytes += boundary_bytes(before, max(width, 0), ev["after"], ev["freed"], a.layers)
-                    self.boundaries += 1
+                ge._start_boundary(st, i + 1, e, n, n - 256, self.alloc)
+                if account:
+                    self.started.append((i, n))
         # Allocate the new token's slot (SGLang's allocator), then the CSR for every full layer.
         t = self.step_index
         new = self.new_slots[t]
@@ -250,11 +263,24 @@ class Workload:
         for l in range(a.layers):
             ge.decode(self.backend, self.q[l].view(bs, -1), self.layer_objs[l], fb, self.sinks[l],
                       self.o[l].view(bs, -1))
-        if account:
-            res = [self.resident(i) for i in range(bs)]
-            self.resident_hist.append(sum(res) / bs)
-            self.bytes += a.layers * sum(decode_bytes(r) for r in res)
+        # This step's resident counts depend on the boundaries it queued: counted once they finish.
+        self.unaccounted = list(self.lens) if account else None
         self.step_index += 1
+
+    def account_decode(self):
+        """Decode bytes of the last step, from the entries as its boundaries left them."""
+        if self.unaccounted is None:
+            return
+        res = [e["count"] + n - e["frontier"] for e, n in zip(self.entries, self.unaccounted)]
+        self.resident_hist.append(sum(res) / len(res))
+        self.bytes += self.args.layers * sum(decode_bytes(r) for r in res)
+        self.unaccounted = None
+
+    def finish(self):
+        """Finish the queued boundaries and count what the timed steps did."""
+        self.ge.finish_boundaries(self.st)
+        self.account_decode()
+        self.account_boundaries()
 
     def max_resident_list(self):
         # The split plan needs an upper bound of each row's resident count.
@@ -553,12 +579,14 @@ def main():
     w = Workload(args, torch, ge)
     for _ in range(args.warmup):
         w.step(account=False)
+    ge.finish_boundaries(w.st)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
     for _ in range(args.steps):
         w.step(account=True)
+    w.finish()
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0

@@ -29,6 +29,7 @@ constexpr int FUSED_THREADS = 64 * MAX_KVH;
 
 GSE_DEVICE uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
+
 // Keys per workgroup for P workgroups over T keys (0 when T == 0).
 GSE_DEVICE int fused_chunk(int T, int P) { return (T + P - 1) / P; }
 
@@ -281,17 +282,24 @@ struct MergeArgs {
   int bs, q_heads, nparts;  // nparts = P, the fused kernel's workgroup count
 };
 
-// Grid (bs), MERGE_THREADS threads: thread (head t/16, dims [4*(t%16), +4)) merges the
-// partials of its head with the sink:
+// Grid (bs, q_heads / MERGE_HEADS), MERGE_THREADS threads: thread (head 8*y + t/16, dims
+// [4*(t%16), +4)) merges the partials of its head with the sink:
 //   o = sum_w 2^(m_w - M) o_w / (2^(sink - M) + sum_w 2^(m_w - M) l_w), M the maximum,
 // MERGE_BATCH partials at a time with all their loads in flight together (a partial past
 // the range is read again with weight 0), one rescale of the running sums per batch.
-constexpr int MERGE_THREADS = 1024;
+// A sequence's head groups run in separate workgroups, so its queue count is advanced by the
+// last of them to finish: each adds one arrival ticket (bit 24 up) to the count word after it
+// has read the count, and the one that sees every other ticket there removes the tickets and
+// adds the step. The count's low 24 bits never change while a group can still read them.
+constexpr int MERGE_HEADS = 8;
+constexpr int MERGE_THREADS = MERGE_HEADS * 16;
 constexpr int MERGE_BATCH = 8;
+constexpr int32_t QUEUE_TICKET = 1 << 24;
+constexpr int32_t QUEUE_COUNT_MASK = QUEUE_TICKET - 1;
 
 __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(MergeArgs a) {
   const int b = blockIdx.x;
-  const int h = threadIdx.x >> 4;
+  const int h = blockIdx.y * MERGE_HEADS + (threadIdx.x >> 4);
   const int j = threadIdx.x & 15;
   // Independent loads first: the queue slot (row -> mode, count) and the partial range
   // (indptr) are two short chains issued together.
@@ -301,7 +309,7 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(MergeArgs a
   if (a.qq) {
     row = load_index_dyn(a.rows, a.rows_dtype, b);
     const int md = a.mode[row];
-    slot = a.qcount[row];
+    slot = a.qcount[row] & QUEUE_COUNT_MASK;
     queue = md == 1 || md == 2;
   }
   const bool live = h < a.q_heads;
@@ -343,22 +351,28 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(MergeArgs a
     }
     mx = m_new;
   }
-  // Every thread has read the queue slot before thread 0 advances it.
+  if (live) {
+    const float inv = 1.f / lsum;
+    uint2 out;
+    out.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    out.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    *reinterpret_cast<uint2*>(a.o + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + 4 * j) = out;
+    const float norm = (mx + __log2f(lsum)) * kLn2;
+    if (j == 0) a.norm_out[int64_t(b) * a.q_heads + h] = norm;
+    if (queue && slot < a.cap) {
+      const int64_t e = row * a.cap + slot;
+      *reinterpret_cast<uint2*>(a.qq + (e * a.q_heads + h) * D + 4 * j) = qv;
+      if (j == 0) a.qnorm[e * a.q_heads + h] = norm;
+      if (threadIdx.x == 0 && blockIdx.y == 0) a.qlim[e] = end - start;
+    }
+  }
+  if (!queue) return;
+  // Every thread of this group has read the count before its ticket goes in.
   __syncthreads();
-  if (queue && threadIdx.x == 0) a.qcount[row] = slot + 1;
-  if (!live) return;
-  const float inv = 1.f / lsum;
-  uint2 out;
-  out.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
-  out.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
-  *reinterpret_cast<uint2*>(a.o + int64_t(b) * a.o_sb + int64_t(h) * a.o_sh + 4 * j) = out;
-  const float norm = (mx + __log2f(lsum)) * kLn2;
-  if (j == 0) a.norm_out[int64_t(b) * a.q_heads + h] = norm;
-  if (queue && slot < a.cap) {
-    const int64_t e = row * a.cap + slot;
-    *reinterpret_cast<uint2*>(a.qq + (e * a.q_heads + h) * D + 4 * j) = qv;
-    if (j == 0) a.qnorm[e * a.q_heads + h] = norm;
-    if (threadIdx.x == 0) a.qlim[e] = end - start;
+  if (threadIdx.x == 0) {
+    const int groups = gridDim.y;
+    const int32_t before = atomicAdd(a.qcount + row, QUEUE_TICKET);
+    if ((before >> 24) == groups - 1) atomicAdd(a.qcount + row, 1 - groups * QUEUE_TICKET);
   }
 }
 
@@ -604,7 +618,8 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   m.bs = bs;
   m.q_heads = q_heads;
   m.nparts = P;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(bs), dim3(MERGE_THREADS), 0, s, m);
+  const dim3 mgrid(static_cast<uint32_t>(bs), static_cast<uint32_t>((q_heads + MERGE_HEADS - 1) / MERGE_HEADS));
+  hipLaunchKernelGGL(decode_merge_kernel, mgrid, dim3(MERGE_THREADS), 0, s, m);
   if ((rc = gse_launch_check("decode_merge"))) return rc;
 
   if (score_mode == GSE_SCORE_EAGER) {

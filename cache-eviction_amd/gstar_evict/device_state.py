@@ -52,19 +52,56 @@ class State:
         self._ws = {}
         self._status_host = None
         self._pools = None
+        self.pending = []  # boundaries queued on the device whose host part is still to do
+        self._rows_host = self._rows_dev = self._rows_copied = None
 
     def workspace(self, name, nbytes):
         """A cached device byte buffer of at least nbytes (grows, never shrinks)."""
         buf = self._ws.get(name)
         if buf is None or buf.numel() < nbytes:
-            buf = self._ws[name] = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=self.device)
+            # An eighth of headroom, in 2 MiB steps: a row's boundary workspace grows with its
+            # candidates, and each growth is a device allocation.
+            size = max(int(nbytes), 256) if buf is None else max(int(nbytes), buf.numel() + buf.numel() // 8)
+            size = -(-size // (1 << 21)) << 21 if size > (1 << 21) else size
+            del buf
+            self._ws.pop(name, None)
+            buf = self._ws[name] = torch.empty(size, dtype=torch.uint8, device=self.device)
         return buf
 
-    def status_host(self):
-        """A pinned host copy target for a boundary's status words (reused)."""
+    def status_host(self, row):
+        """The pinned host copy target of a boundary's status words, one per row (a row has at
+        most one boundary in flight: its next one is a whole interval later and every hook
+        finishes pending boundaries first)."""
         if self._status_host is None:
-            self._status_host = torch.zeros(16, dtype=torch.int32, pin_memory=True)
-        return self._status_host
+            self._status_host = torch.zeros((self.req_to_token.shape[0], 16), dtype=torch.int32, pin_memory=True)
+        return self._status_host[row]
+
+    def row_list(self, rows):
+        """``rows`` (host ints) as a device int32 vector, through a persistent pinned buffer: the
+        copy is queued on the current stream and the buffer is reused once the previous copy from
+        it has completed (a multi-row flush is a few per interval, so that wait never blocks)."""
+        n = len(rows)
+        if self._rows_host is None:
+            self._pin_rows()
+        else:
+            self._rows_copied.synchronize()
+        self._rows_host[:n] = torch.tensor(rows, dtype=torch.int32)
+        self._rows_dev[:n].copy_(self._rows_host[:n], non_blocking=True)
+        self._rows_copied.record()
+        return self._rows_dev[:n]
+
+    def _pin_rows(self):
+        if self._rows_host is None:
+            total = self.req_to_token.shape[0]
+            self._rows_host = torch.zeros(total, dtype=torch.int32, pin_memory=True)
+            self._rows_dev = torch.zeros(total, dtype=torch.int32, device=self.device)
+            self._rows_copied = torch.cuda.Event()
+
+    def finish_pending(self):
+        """Do the host part of every queued boundary, oldest first."""
+        from .compaction import finish_boundary
+        while self.pending:
+            finish_boundary(self, self.pending.pop(0))
 
     def ensure_queue(self):
         """Allocate the score queues once (the decode kernels fix 8 query heads per KV head)."""
@@ -75,6 +112,10 @@ class State:
         self.qq = torch.zeros((layers, n_rows, cap, self.q_heads, self.dim), dtype=torch.bfloat16, device=self.device)
         self.qnorm = torch.zeros((layers, n_rows, cap, self.q_heads), dtype=torch.float32, device=self.device)
         self.qlim = torch.zeros((layers, n_rows, cap), dtype=torch.int32, device=self.device)
+        # Pinned host buffers now, at the first decode step: allocating pinned memory
+        # synchronises the device, which would drain the GPU if done mid-run.
+        self.status_host(0)
+        self._pin_rows()
 
     def pool_pointers(self):
         """Device arrays of the full layers' K and V buffer addresses, and their shared strides."""
@@ -93,6 +134,7 @@ class State:
     def release_row(self, row):
         """Forget a row: its entry, policy mode, eviction state and queued decode steps (queued
         scores must not land on slots the row no longer owns)."""
+        self.finish_pending()
         self.entries.pop(row, None)
         for t in (self.mode, self.frontier, self.count):
             t[row] = 0

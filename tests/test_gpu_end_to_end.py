@@ -4,7 +4,8 @@ One full-attention layer (64 query heads, 8 KV heads, d=64), Q/K/V ~ N(0, 1) fro
 scale 1/sqrt(64), sink logits ~ N(0, 1). A 4096-token prompt arrives in two 2048-token
 chunks (`on_extend` + `after_extend`), then decode steps run `on_decode`, `fill` and the
 fused `decode`; the boundary at 4096 fires at the first decode step with head_sum at budget
-2048 = 128 prefix + 512 recent + 1408 scored. Every stage is compared with the oracle: prefill
+2048 = 128 prefix + 512 recent + 1408 scored. `on_decode` queues it and the next `on_decode`
+does its host part, so the device state is checked in between and the entry after. Every stage is compared with the oracle: prefill
 scores, the boundary's retained positions, table, req_to_token, relocated K/V/scores and freed
 slots (bit-exact, the oracle ranking the GPU's own pre-boundary scores), each step's attention
 output, and the accumulated scores after the last step.
@@ -132,17 +133,24 @@ def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang):
         ge.on_decode(SimpleNamespace(reqs=[req], seq_lens_cpu=torch.tensor([p]),
                                      tree_cache=SimpleNamespace(token_to_kv_pool_allocator=alloc)))
         if t == 0:
+            # The boundary is queued, its host part pending: the device state is already its
+            # outcome, the entry and the allocator are not yet.
             ofreed = []
             O.boundary(ost, ROW, oe, p, p - 128, free=ofreed.append)
-            torch.cuda.synchronize()
-            assert entry["count"] == oe["count"] == BUDGET
-            _assert_same_positions(entry["pos"].cpu().numpy(), oe["pos"], pre_scores, slot_of.cpu().numpy())
+            assert len(st.pending) == 1 and entry["count"] == 0 and not freed
             assert np.array_equal(st.table[ROW, :BUDGET].cpu().numpy(), ost.table[ROW, :BUDGET])
             assert np.array_equal(st.req_to_token[ROW].cpu().numpy(), ost.req_to_token[ROW])
+            assert int(st.count[ROW]) == BUDGET and int(st.frontier[ROW]) == p
             assert np.array_equal(keys.float().cpu().numpy(), ost.keys[0])
             assert np.array_equal(values.float().cpu().numpy(), ost.values[0])
             assert np.array_equal(st.scores.cpu().numpy(), ost.scores)
+        if t == 1:
+            # The next decode hook finished it.
+            assert not st.pending
+            assert entry["count"] == oe["count"] == BUDGET and entry["frontier"] == PROMPT
+            _assert_same_positions(entry["pos"].cpu().numpy(), oe["pos"], pre_scores, slot_of.cpu().numpy())
             assert np.array_equal(torch.cat(freed).cpu().numpy(), ofreed[0])
+            assert [ev["after"] for ev in entry["events"]][-1] == BUDGET
         # SGLang's allocation of the new token, then the CSR and the fused decode.
         new = slot_of[p:p + 1]
         st.req_to_token[ROW, p] = new.int()
