@@ -72,7 +72,7 @@ def test_fill_matches_oracle_on_random_rows():
 
 def _decode_setup(lengths, seed=0, slots=20000):
     g = torch.Generator().manual_seed(seed)
-    b = backend(gen=g, slots=slots)
+    b = backend(gen=g, slots=slots, rows=max(4, len(lengths) + 1))  # rows 1..bs
     st = ge.state(b)
     heads, kv_heads, dim = 64, 8, 64
     bs = len(lengths)
@@ -249,3 +249,41 @@ def test_full_queues_flush_before_the_step(monkeypatch, mode):
         assert int(st.qcount.abs().sum()) == 0
         results[score_mode] = st.scores.clone()
     torch.testing.assert_close(results["queue"], results["eager"], rtol=1e-5, atol=1e-8)
+
+
+def test_merge_of_empty_short_and_long_sequences_over_a_reused_workspace():
+    """The merge of a batch with empty sequences (all mass on the sink: o = 0, normaliser =
+    sink, queued with list length 0), one inside a single workgroup and one across many; then a
+    smaller batch on the same workspace. Each row's queue count is exactly one step after its
+    head groups' arrival tickets are taken back."""
+    for call, lengths in enumerate(([0, 5, 4000, 0, 1], [300, 2])):
+        b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths, seed=20 + call)
+        if call:
+            st._ws = keep  # the previous call's workspace
+        st.score_mode = "queue"
+        st.mode[:] = 1
+        b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=perm)
+        fb = SimpleNamespace(out_cache_loc=torch.zeros(len(lengths), dtype=torch.int64, device="cuda"),
+                             req_pool_indices=rows, seq_lens_cpu=torch.tensor(lengths))
+        o = torch.full_like(q, float("nan"))
+        assert ge.decode(b, q.reshape(len(lengths), -1), layer(1), fb, sinks, o.reshape(len(lengths), -1))
+        keep = st._ws
+        got = o.float().cpu().numpy()
+        keys = b.token_to_kv_pool.get_key_buffer(1).float().cpu().numpy()
+        values = b.token_to_kv_pool.get_value_buffer(1).float().cpu().numpy()
+        ip, pm, sn = indptr.cpu().numpy(), perm.cpu().numpy(), sinks.float().cpu().numpy()
+        index = st.index[1]
+        for i, n in enumerate(lengths):
+            row = int(rows[i])
+            assert int(st.qcount[index, row]) == 1
+            assert int(st.qlim[index, row, 0]) == n
+            if n == 0:
+                assert np.all(got[i] == 0.0)
+                np.testing.assert_allclose(st.qnorm[index, row, 0].cpu().numpy(), sn, rtol=1e-6, atol=1e-6)
+                continue
+            want_o, want_norm = O.decode_attention(q[i].float().cpu().numpy(), keys, values, pm[ip[i]:ip[i + 1]], sn,
+                                                   0.125)
+            np.testing.assert_allclose(got[i], want_o, rtol=2e-2, atol=2e-2)
+            np.testing.assert_allclose(st.qnorm[index, row, 0].cpu().numpy(), want_norm, rtol=1e-5, atol=1e-4)
+        assert torch.equal(st.qq[index, rows, 0], q)
+        ge.STATE = None
