@@ -109,6 +109,7 @@ struct SelArgs {
   int layers, kv_heads;
   int64_t n_cols, n, budget, prefix, recent, cursor;
   int has_cursor, prefix_sliding, boundary_mode;
+  int block;  // tokens per eviction block (1: token granularity)
   uint64_t* keys;     // [LG, N]
   int32_t* posw;      // [LG, N]; protected stored as ~pos
   int32_t* prot_count;
@@ -120,8 +121,28 @@ struct SelArgs {
   int nwords;         // ceil(n / 32) position bitmap words
 };
 
-GSE_DEVICE bool is_protected(const SelArgs& a, int64_t p) {
+GSE_DEVICE bool is_protected_pos(const SelArgs& a, int64_t p) {
   return p < a.prefix || p >= a.n - a.recent || (a.has_cursor && p >= a.cursor);
+}
+
+// Block policies protect a whole block when any of its positions is protected: the protected
+// positions are a prefix and a suffix of [0, n), so the block's first and last positions decide.
+GSE_DEVICE bool is_protected(const SelArgs& a, int64_t p) {
+  if (a.block <= 1) return is_protected_pos(a, p);
+  const int64_t first = p - p % a.block;
+  return is_protected_pos(a, first) || is_protected_pos(a, first + a.block - 1);
+}
+
+// Kept unprotected columns: the budget left after the protected set, whole blocks only.
+GSE_DEVICE int64_t kept_width(int64_t budget, int64_t protected_count, int block, int prefix_sliding) {
+  if (prefix_sliding) return 0;
+  const int64_t w = budget - protected_count;
+  return block > 1 && w > 0 ? w - w % block : w;
+}
+
+GSE_DEVICE bool f64_policy(int policy) {
+  return policy == GSE_POLICY_RESERVOIR || policy == GSE_POLICY_RANDOM || policy == GSE_POLICY_BLOCK_SUM ||
+         policy == GSE_POLICY_BLOCK_MAX;
 }
 
 // Rank of position p among the set bits of the LDS bitmap: block prefix + in-block popcounts.
@@ -180,7 +201,8 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
         sc = a.src.score[int64_t(lg) * N + c];
       } else if (a.src.policy == GSE_POLICY_RESERVOIR) {
         sc = double(splitmix_bits(a.src.seed, l, g, p)) / 9007199254740992.0;
-      } else if (a.src.policy == GSE_POLICY_RANDOM) {
+      } else if (a.src.policy == GSE_POLICY_RANDOM || a.src.policy == GSE_POLICY_BLOCK_SUM ||
+                 a.src.policy == GSE_POLICY_BLOCK_MAX) {
         sc = a.src.random_scores[int64_t(lg) * N + c];
       } else {
         sc = double(a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg +
@@ -193,7 +215,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
   const int P = block_sum(nprot, tmp);
   if (threadIdx.x == 0) a.prot_count[lg] = P;
   const int64_t M = N - P;
-  int64_t k = a.prefix_sliding ? 0 : a.budget - P;
+  int64_t k = kept_width(a.budget, P, a.block, a.prefix_sliding);
   if (k < 0) k = 0;  // deferred: keep nothing beyond the protected set
   if (k > M) k = M;
 
@@ -329,7 +351,8 @@ GSE_DEVICE int32_t col_pos(const SelArgs& a, int lg, int64_t c) {
 GSE_DEVICE uint64_t col_key64(const SelArgs& a, int l, int g, int lg, int64_t c, int32_t p) {
   if (a.src.policy == GSE_POLICY_RESERVOIR)
     return ordered_f64(double(splitmix_bits(a.src.seed, l, g, p)) / 9007199254740992.0);
-  if (a.src.policy == GSE_POLICY_RANDOM) return ordered_f64(a.src.random_scores[int64_t(lg) * a.n_cols + c]);
+  if (a.src.policy == GSE_POLICY_RANDOM || a.src.policy == GSE_POLICY_BLOCK_SUM || a.src.policy == GSE_POLICY_BLOCK_MAX)
+    return ordered_f64(a.src.random_scores[int64_t(lg) * a.n_cols + c]);
   if (a.src.policy == GSE_POLICY_PREFIX_SLIDING) return uint64_t(ordered_f32(0.f)) << 32;
   const float sc = a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg + int64_t(a.src.slots[c]) * a.src.sss];
   return uint64_t(ordered_f32(sc)) << 32;
@@ -373,7 +396,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
   const int l = lg / a.kv_heads, g = lg % a.kv_heads;
   const int N = int(a.n_cols);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const bool f64 = a.src.policy == GSE_POLICY_RESERVOIR || a.src.policy == GSE_POLICY_RANDOM;
+  const bool f64 = f64_policy(a.src.policy);
   const bool table_scores = !f64 && !a.prefix_sliding;
   auto col = [&](int k) { return int(threadIdx.x) + k * SEL_THREADS; };
 
@@ -443,7 +466,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
   }
   if (threadIdx.x == 0) a.prot_count[lg] = P;
   const int M = N - P;
-  int k = a.prefix_sliding ? 0 : int(a.budget) - P;
+  int k = int(kept_width(a.budget, P, a.block, a.prefix_sliding));
   if (k < 0) k = 0;  // deferred: keep nothing beyond the protected set
   if (k > M) k = M;
 
@@ -612,6 +635,7 @@ struct BndArgs {
   int layers, kv_heads, head_dim;
   int64_t N, n, budget;
   int prefix_sliding;
+  int block;  // tokens per eviction block (the kept width is whole blocks)
   const int32_t* table_in;  // read by prep only
   int32_t* table;
   int64_t table_stride;
@@ -685,7 +709,7 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
     int state = GSE_BOUNDARY_EVICTED;
     if (mn != mx) state = GSE_BOUNDARY_ERR_HEADS;
     else if (P > a.budget) state = GSE_BOUNDARY_DEFERRED;
-    const int64_t width = a.prefix_sliding ? 0 : a.budget - P;
+    const int64_t width = kept_width(a.budget, P, a.block, a.prefix_sliding);
     bc[0] = state;
     bc[1] = P;
     bc[2] = int(width);
@@ -872,6 +896,77 @@ __global__ __launch_bounds__(256) void protected_pos_kernel(BndArgs a) {
   }
 }
 
+// ------------------------------------------------------ block policy scores --
+//
+// block_sum_2048 / block_max_2048 rank whole blocks of `block` consecutive positions. A
+// block's score is the float64 sum (or max) of its positions' table scores, taken in a fixed
+// order: positions ascending, then, for a layer-shared choice, KV heads ascending (absent
+// positions add 0). Every column gets its block's score and the selection kernels rank them
+// as float64 scores; protection covers whole blocks (is_protected) and the kept width is
+// whole blocks (kept_width).
+
+struct BlkArgs {
+  int layers, kv_heads, block, shared, max_mode;
+  int64_t N, n, nblocks;
+  int64_t count, frontier;
+  const int32_t* pos_old;
+  int64_t pstride;
+  const int32_t* slots;
+  const float* scores;
+  int64_t ssl, ssg, sss;
+  float* bypos;     // [LG, n] table score by position
+  double* bscore;   // [units, nblocks], units = layers (shared) or LG
+  double* colscore; // [LG, N]
+};
+
+GSE_DEVICE int64_t blk_pos(const BlkArgs& b, int lg, int64_t c) {
+  return c < b.count ? int64_t(b.pos_old[int64_t(lg) * b.pstride + c]) : b.frontier + c - b.count;
+}
+
+__global__ void block_clear_kernel(float* p, int64_t total) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x)
+    p[i] = 0.f;
+}
+
+// Grid (ceil(N / 256), LG).
+__global__ void block_scatter_kernel(BlkArgs b) {
+  const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int lg = blockIdx.y;
+  if (c >= b.N) return;
+  const int l = lg / b.kv_heads, g = lg % b.kv_heads;
+  const int64_t p = blk_pos(b, lg, c);
+  if (p < 0 || p >= b.n) return;
+  b.bypos[int64_t(lg) * b.n + p] = b.scores[int64_t(l) * b.ssl + int64_t(g) * b.ssg + int64_t(b.slots[c]) * b.sss];
+}
+
+// Grid (ceil(nblocks / 256), units).
+__global__ void block_score_kernel(BlkArgs b) {
+  const int64_t bi = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int u = blockIdx.y;
+  if (bi >= b.nblocks) return;
+  const int l = b.shared ? u : u / b.kv_heads;
+  const int g0 = b.shared ? 0 : u % b.kv_heads, g1 = b.shared ? b.kv_heads : g0 + 1;
+  double s = 0.0;
+  const int64_t first = bi * b.block;
+  for (int i = 0; i < b.block && first + i < b.n; ++i)
+    for (int g = g0; g < g1; ++g) {
+      const double v = double(b.bypos[(int64_t(l) * b.kv_heads + g) * b.n + first + i]);
+      s = b.max_mode ? fmax(s, v) : s + v;
+    }
+  b.bscore[int64_t(u) * b.nblocks + bi] = s;
+}
+
+// Grid (ceil(N / 256), LG).
+__global__ void block_column_kernel(BlkArgs b) {
+  const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int lg = blockIdx.y;
+  if (c >= b.N) return;
+  const int64_t p = blk_pos(b, lg, c);
+  const int u = b.shared ? lg / b.kv_heads : lg;
+  const int64_t bi = p >= 0 && p < b.n ? p / b.block : 0;
+  b.colscore[int64_t(lg) * b.N + c] = b.bscore[int64_t(u) * b.nblocks + bi];
+}
+
 // ---------------------------------------------------------- live compaction --
 
 struct LiveArgs {
@@ -984,13 +1079,23 @@ namespace {
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 struct BndLayout {
-  int64_t slots, keys, posw, prot, middle, prot_cols, targets, skv, ssc, total;
+  int64_t slots, keys, posw, prot, middle, prot_cols, targets, skv, ssc, bypos, bscore, colscore, total;
 };
 
-BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t budget) {
+bool block_policy(int policy) { return policy == GSE_POLICY_BLOCK_SUM || policy == GSE_POLICY_BLOCK_MAX; }
+
+// Block policies add the position-indexed scratch ([LG, n] scores, [LG, ceil(n / block)] block
+// scores, [LG, N] column scores).
+BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t n, int64_t budget, int policy,
+                     int block) {
   const int64_t LG = int64_t(layers) * kv_heads;
+  const bool blk = block_policy(policy);
+  const int64_t nblocks = blk && block > 0 ? (n + block - 1) / block : 0;
   BndLayout L;
   int64_t o = 0;
+  L.bypos = o; o += blk ? align256(LG * n * 4) : 0;
+  L.bscore = o; o += blk ? align256(LG * nblocks * 8) : 0;
+  L.colscore = o; o += blk ? align256(LG * N * 8) : 0;
   L.slots = o; o += align256(((N + 31) / 32) * 32 * 4);  // whole 32-column words
   L.keys = o; o += align256(LG * N * 8);
   L.posw = o; o += align256(LG * N * 4);
@@ -1012,9 +1117,8 @@ size_t select_lds_bytes(int nwords) {
 }  // namespace
 
 extern "C" int64_t gse_boundary_workspace_bytes(int layers, int kv_heads, int head_dim, int64_t n_cols, int64_t n,
-                                                int64_t budget) {
-  (void)n;
-  return bnd_layout(layers, kv_heads, head_dim, n_cols, budget).total;
+                                                int64_t budget, int policy, int block) {
+  return bnd_layout(layers, kv_heads, head_dim, n_cols, n, budget, policy, block).total;
 }
 
 extern "C" int64_t gse_boundary_live_workspace_bytes(int64_t num_slots) { return align256(((num_slots + 31) / 32) * 4); }
@@ -1072,7 +1176,8 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
                             const int32_t* req_to_token, int64_t r2t_stride, int32_t* frontier, int32_t* count, int row,
                             int64_t row_count, int64_t row_frontier, const int32_t* pos_old, int64_t pos_old_stride,
                             int64_t n, int64_t budget, int64_t prefix, int64_t recent, int64_t cursor, int has_cursor,
-                            int policy, int64_t seed, const double* random_scores, int32_t* pos_new,
+                            int policy, int64_t seed, int block, int shared, const double* random_scores,
+                            int32_t* pos_new,
                             int64_t* leftover, gse_boundary_status* status, void* workspace, int64_t workspace_bytes,
                             gse_stream_t stream) {
   const int64_t N = row_count + n - row_frontier;
@@ -1082,13 +1187,15 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
     return gse_fail(GSE_ESHAPE, "boundary: head_dim and K/V strides must be multiples of 8");
   if (n > MAX_POSITIONS || N >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "boundary: logical length too large");
   if (row_count > 0 && !pos_old) return gse_fail(GSE_EINVAL, "boundary: pos_old needed when count > 0");
-  if (policy < GSE_POLICY_HEAD_SUM || policy > GSE_POLICY_PREFIX_SLIDING)
-    return gse_fail(GSE_EINVAL, "boundary: unknown policy");
+  if (policy < GSE_POLICY_HEAD_SUM || policy > GSE_POLICY_BLOCK_MAX) return gse_fail(GSE_EINVAL, "boundary: unknown policy");
+  const bool blk = block_policy(policy);
+  if (blk ? (block < 1 || block > 2048) : (block != 1 || shared))
+    return gse_fail(GSE_EINVAL, "boundary: block must be 1..2048 for block policies, 1 (not shared) for others");
   if (policy == GSE_POLICY_RANDOM && !random_scores) return gse_fail(GSE_EINVAL, "boundary: random_2048 needs scores");
   if (!k_pools || !v_pools || !scores || !table || !req_to_token || !frontier || !count || !pos_new || !leftover ||
       !status)
     return gse_fail(GSE_EINVAL, "boundary: null pointer");
-  const BndLayout L = bnd_layout(layers, kv_heads, head_dim, N, budget);
+  const BndLayout L = bnd_layout(layers, kv_heads, head_dim, N, n, budget, policy, block);
   if (workspace_bytes < L.total) return gse_fail(GSE_EWORKSPACE, "boundary: workspace too small");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
@@ -1102,6 +1209,7 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   b.n = n;
   b.budget = budget;
   b.prefix_sliding = policy == GSE_POLICY_PREFIX_SLIDING;
+  b.block = block;
   b.table = table;
   b.table_stride = table_stride;
   b.r2t = req_to_token;
@@ -1136,6 +1244,42 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   hipLaunchKernelGGL(prep_slots_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, s, b);
   if (int rc = gse_launch_check("boundary prep")) return rc;
 
+  const double* f64_scores = random_scores;
+  if (blk) {
+    BlkArgs k = {};
+    k.layers = layers;
+    k.kv_heads = kv_heads;
+    k.block = block;
+    k.shared = shared ? 1 : 0;
+    k.max_mode = policy == GSE_POLICY_BLOCK_MAX;
+    k.N = N;
+    k.n = n;
+    k.nblocks = (n + block - 1) / block;
+    k.count = row_count;
+    k.frontier = row_frontier;
+    k.pos_old = pos_old;
+    k.pstride = pos_old_stride;
+    k.slots = b.slots;
+    k.scores = scores;
+    k.ssl = scores_stride_l;
+    k.ssg = scores_stride_g;
+    k.sss = scores_stride_s;
+    k.bypos = reinterpret_cast<float*>(ws + L.bypos);
+    k.bscore = reinterpret_cast<double*>(ws + L.bscore);
+    k.colscore = reinterpret_cast<double*>(ws + L.colscore);
+    hipLaunchKernelGGL(block_clear_kernel, dim3(1024), dim3(256), 0, s, k.bypos, int64_t(LG) * n);
+    if (int rc = gse_launch_check("boundary block clear")) return rc;
+    const dim3 cgrid(unsigned((N + 255) / 256), unsigned(LG));
+    hipLaunchKernelGGL(block_scatter_kernel, cgrid, dim3(256), 0, s, k);
+    if (int rc = gse_launch_check("boundary block scatter")) return rc;
+    hipLaunchKernelGGL(block_score_kernel, dim3(unsigned((k.nblocks + 255) / 256), unsigned(shared ? layers : LG)),
+                       dim3(256), 0, s, k);
+    if (int rc = gse_launch_check("boundary block scores")) return rc;
+    hipLaunchKernelGGL(block_column_kernel, cgrid, dim3(256), 0, s, k);
+    if (int rc = gse_launch_check("boundary block columns")) return rc;
+    f64_scores = k.colscore;
+  }
+
   SelArgs a = {};
   a.src.pos_old = pos_old;
   a.src.pstride = pos_old_stride;
@@ -1147,7 +1291,7 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   a.src.ssg = scores_stride_g;
   a.src.sss = scores_stride_s;
   a.src.slots = b.slots;
-  a.src.random_scores = random_scores;
+  a.src.random_scores = f64_scores;
   a.src.seed = seed;
   a.layers = layers;
   a.kv_heads = kv_heads;
@@ -1160,6 +1304,7 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   a.has_cursor = has_cursor;
   a.prefix_sliding = b.prefix_sliding;
   a.boundary_mode = 1;
+  a.block = block;
   a.keys = reinterpret_cast<uint64_t*>(ws + L.keys);
   a.posw = reinterpret_cast<int32_t*>(ws + L.posw);
   a.prot_count = b.prot_count;

@@ -19,7 +19,7 @@ I32, I64 = 0, 1
 F32, BF16 = 0, 1
 SCORE_NONE, SCORE_EAGER, SCORE_QUEUE = 0, 1, 2
 POLICY_IDS = {"head_sum_2048": 1, "head_max_sum_2048": 2, "random_2048": 3,
-              "random_reservoir_2048": 4, "prefix_sliding_2048": 5}
+              "random_reservoir_2048": 4, "prefix_sliding_2048": 5, "block_sum_2048": 6, "block_max_2048": 7}
 BOUNDARY_EVICTED, BOUNDARY_DEFERRED, BOUNDARY_ERR_HEADS, BOUNDARY_ERR_SWA, BOUNDARY_ERR_PACKED = 0, 2, 3, 4, 5
 
 _p, _i, _l, _f, _d = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double
@@ -39,9 +39,9 @@ SIGNATURES = {
                                         _p, _p, _i, _p, _l, _l, _i, _i, _i, _i, _f, _i, _p, _l, _p]),
     "gse_reservoir_scores": (_i, [_p, _i, _p, _p, _i, _i, _l, _l, _p, _p]),
     "gse_select_kept": (_i, [_p, _p, _i, _i, _l, _l, _l, _l, _l, _l, _i, _i, _p, _p, _p, _l, _p]),
-    "gse_boundary_workspace_bytes": (_l, [_i, _i, _i, _l, _l, _l]),
+    "gse_boundary_workspace_bytes": (_l, [_i, _i, _i, _l, _l, _l, _i, _i]),
     "gse_boundary": (_i, [_p, _p, _i, _l, _l, _i, _i, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _i, _l, _l, _p, _l,
-                          _l, _l, _l, _l, _l, _i, _i, _l, _p, _p, _p, _p, _p, _l, _p]),
+                          _l, _l, _l, _l, _l, _i, _i, _l, _i, _i, _p, _p, _p, _p, _p, _l, _p]),
     "gse_boundary_live_workspace_bytes": (_l, [_l]),
     "gse_boundary_live": (_i, [_p, _i, _l, _i, _l, _l, _p, _l, _p, _l, _i, _l, _l, _p, _p, _i, _l, _p, _p, _l, _p]),
     "gse_prefill_workspace_bytes": (_l, [_l, _i]),

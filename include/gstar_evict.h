@@ -42,7 +42,10 @@ enum {
   GSE_POLICY_HEAD_MAX_SUM = 2,     /* head_max_sum_2048: same gather                   */
   GSE_POLICY_RANDOM = 3,           /* random_2048: caller-drawn float64 scores          */
   GSE_POLICY_RESERVOIR = 4,        /* random_reservoir_2048: splitmix64 in-kernel       */
-  GSE_POLICY_PREFIX_SLIDING = 5    /* prefix_sliding_2048: protected set only           */
+  GSE_POLICY_PREFIX_SLIDING = 5,   /* prefix_sliding_2048: protected set only           */
+  GSE_POLICY_BLOCK_SUM = 6,        /* block_sum_2048 (no reference counterpart): a block's
+                                      score is the sum of its table scores              */
+  GSE_POLICY_BLOCK_MAX = 7         /* block_max_2048 (no reference counterpart): the max */
 };
 
 /* Decode score modes of gse_decode. */
@@ -194,9 +197,10 @@ int gse_select_kept(const int32_t* pos, const double* score, int layers, int kv_
                     int prefix_sliding, uint8_t* kept_mask, int32_t* prot_count, void* workspace,
                     int64_t workspace_bytes, gse_stream_t stream);
 
-/* Workspace bytes gse_select_kept and gse_boundary need (n_cols = N columns, n = logical length). */
+/* Workspace bytes gse_boundary needs (n_cols = N columns, n = logical length; policy and
+ * block as passed to gse_boundary). */
 int64_t gse_boundary_workspace_bytes(int layers, int kv_heads, int head_dim, int64_t n_cols, int64_t n,
-                                     int64_t budget);
+                                     int64_t budget, int policy, int block);
 
 /*
  * boundary — ranking half of one row's eviction boundary at logical length n.
@@ -213,6 +217,14 @@ int64_t gse_boundary_workspace_bytes(int layers, int kv_heads, int head_dim, int
  * `count` columns valid), leftover slots (int64, N - count of them) and
  * *status. Deferred or invalid boundaries (status.state != EVICTED) change no
  * state. Call only when N = row_count + n - row_frontier > budget (R:433-435).
+ * block / shared: 1 / 0 except for the block policies (no reference counterpart;
+ * the block-granular, layer-shared variant of the reference report's ARC-AGI-3
+ * runs), which keep whole blocks of `block` positions (1..2048): a block is
+ * protected if any of its positions is, the kept width is budget - protected
+ * rounded down to whole blocks, and each column ranks by its block's float64
+ * score, the sum (GSE_POLICY_BLOCK_SUM) or max (GSE_POLICY_BLOCK_MAX) of the
+ * table scores of the block's positions ascending and, if shared, of every KV
+ * head of the layer ascending (then all heads of a layer keep the same blocks).
  */
 int gse_boundary(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
                  int kv_heads, int head_dim, float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
@@ -220,7 +232,7 @@ int gse_boundary(void* const* k_pools, void* const* v_pools, int layers, int64_t
                  int32_t* table, int64_t table_stride, const int32_t* req_to_token, int64_t r2t_stride,
                  int32_t* frontier, int32_t* count, int row, int64_t row_count, int64_t row_frontier,
                  const int32_t* pos_old, int64_t pos_old_stride, int64_t n, int64_t budget, int64_t prefix,
-                 int64_t recent, int64_t cursor, int has_cursor, int policy, int64_t seed,
+                 int64_t recent, int64_t cursor, int has_cursor, int policy, int64_t seed, int block, int shared,
                  const double* random_scores, int32_t* pos_new, int64_t* leftover, gse_boundary_status* status,
                  void* workspace, int64_t workspace_bytes, gse_stream_t stream);
 
