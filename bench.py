@@ -53,6 +53,8 @@ def parse(argv=None):
     p.add_argument("--kernel-reps", type=int, default=20, help="launches timed per layer for the roofline")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--eager", action="store_true", help="score each step eagerly (second K pass per step)")
+    p.add_argument("--prefill-policy", default="block_sum_2048",
+                   help="eviction policy of the --prefill workload (block policies: 16-token layer-shared blocks)")
     p.add_argument("--prefill", action="store_true",
                    help="time the chunked-prefill score tiles instead: 12 layers, 79,720-token prompt in "
                         "8192-token chunks, prefix capped at the 28,672-token budget (MFMA roofline)")
@@ -408,72 +410,119 @@ PEAK_BF16_TFLOPS = 2500.0
 
 
 def prefill_bench(args, torch, ge):
-    """Chunked-prefill scoring at the 79,720-token shape: per chunk and layer, exact causal
-    softmax probabilities (sink in the normaliser) summed per KV head onto the keys' scores.
-    Algorithmic work = 2 * 64 heads * 64 dims flop per causal (query, key) pair for one QK^T
-    pass; the kernel issues a second pass (the normaliser first, then the probabilities)."""
+    """Chunked prefill at the 79,720-token shape with eviction: one row prefills 8192-token
+    chunks; before each chunk the row's boundary keeps 512 + 4096 + 24,064 positions with the
+    block policy (16-token blocks chosen per layer, one choice for all KV heads, block score =
+    the sum of its positions' scores; ``--prefill-policy`` picks another), then per chunk and
+    layer the exact causal softmax probabilities (sink in the normaliser) over the row's
+    resident keys are summed per KV head onto the keys' scores.
+    Scoring work = 2 * 64 heads * 64 dims flop per causal (query, key) pair for one QK^T pass
+    (the kernel issues a second pass: the normaliser first, then the probabilities). Boundaries
+    run in replay mode (survivors relocated, nothing freed) and are timed separately."""
     prompt, chunk, cap = 79720, 8192, 512 + 4096 + 24064
     L = args.layers
-    slots = cap + chunk + 64
+    slots = prompt + 64
     g = torch.Generator(device="cuda").manual_seed(args.seed)
     keys, values = {}, {}
     for l in range(L):
-        k = torch.randn((slots, HKV, D), device="cuda", dtype=torch.bfloat16, generator=g)
+        k = torch.randn((slots + 1, HKV, D), device="cuda", dtype=torch.bfloat16, generator=g)
         u = torch.randn((HKV, D), device="cuda", generator=g)
         u = u / u.norm(dim=-1, keepdim=True)
-        heavy = torch.rand((slots, HKV), device="cuda", generator=g) < 0.05
+        heavy = torch.rand((slots + 1, HKV), device="cuda", generator=g) < 0.05
         planted = (4 * k.float().norm(dim=-1, keepdim=True) * u[None]).to(torch.bfloat16)
         keys[l] = torch.where(heavy[..., None], planted, k)
-        values[l] = keys[l]  # values are not read by the score pass
+        values[l] = torch.randn((slots + 1, HKV, D), device="cuda", dtype=torch.bfloat16, generator=g)
     pool = SimpleNamespace(layers_mapping={l: (l, False) for l in range(L)},
                            get_key_buffer=keys.__getitem__, get_value_buffer=values.__getitem__)
+    width = -(-prompt // 256) * 256
     backend = SimpleNamespace(token_to_kv_pool=pool, max_kv_splits=16,
-                              req_to_token_pool=SimpleNamespace(req_to_token=torch.zeros((2, 64), dtype=torch.int32,
+                              req_to_token_pool=SimpleNamespace(req_to_token=torch.zeros((2, width), dtype=torch.int32,
                                                                                          device="cuda")),
                               kv_indptr=torch.zeros(3, dtype=torch.int32, device="cuda"))
     ge.STATE = None
     st = ge.state(backend)
     q = torch.randn((chunk, HQ, D), device="cuda", dtype=torch.bfloat16, generator=g)
     sinks = torch.randn(HQ, device="cuda", generator=g)
-    perm = torch.randperm(slots - 1, device="cuda", generator=g) + 1
+    st.req_to_token[1, :prompt] = (torch.randperm(slots, device="cuda", generator=g)[:prompt] + 1).int()
     layer_objs = [SimpleNamespace(sliding_window_size=-1, tp_q_head_num=HQ, tp_k_head_num=HKV, qk_head_dim=D,
                                   layer_id=l, scaling=D ** -0.5) for l in range(L)]
-    plan = []  # (prefix, count) per chunk; the resident prefix is capped at the budget
-    for start in range(0, prompt, chunk):
-        plan.append((min(start, cap), min(chunk, prompt - start)))
+    cfg = {"name": args.prefill_policy, "budget": cap, "prefix": 512, "recent": 4096, "seed": args.seed}
+    if args.prefill_policy in ("block_sum_2048", "block_max_2048"):
+        cfg.update(block=16, shared=True)
+    mode = 2 if args.prefill_policy in ("head_max_sum_2048", "block_max_2048") else 1
+    starts = list(range(0, prompt, chunk))
+    timing = {"score": [], "boundary": []}
 
-    def run():
-        for prefix, count in plan:
+    def run(record):
+        # A fresh row: no eviction state, zero scores; the pools keep whatever earlier runs moved.
+        st.table.zero_()
+        st.count.zero_()
+        st.frontier.zero_()
+        st.scores.zero_()
+        entry = ge._live_entry(SimpleNamespace(rid="prompt", session=None), cfg, "replay")
+        st.entries[1] = entry
+        st.mode[1] = entry["mode"]
+        resident = []
+        for start in starts:
+            count = min(chunk, prompt - start)
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            ev[0].record()
+            if start:
+                ge._boundary(st, 1, entry, start)
+            ev[1].record()
+            prefix = torch.cat((st.table[1, :entry["count"]], st.req_to_token[1, entry["frontier"]:start]))
+            new = st.req_to_token[1, start:start + count]
             for l in range(L):
-                ge._prefill_scores(st, l, 1, layer_objs[l], q[:count], keys[l], sinks, perm[:prefix],
-                                   perm[prefix:prefix + count])
+                ge._prefill_scores(st, l, mode, layer_objs[l], q[:count], keys[l], sinks, prefix, new)
+            ev[2].record()
+            resident.append(prefix.numel())
+            if record:
+                timing["boundary"].append(ev[:2])
+                timing["score"].append(ev[1:])
+        return entry, resident
 
-    run()
+    run(False)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     reps = max(1, min(args.steps, 3))  # one step is the whole 79,720-token prompt (about a second)
     start.record()
     for _ in range(reps):
-        run()
+        entry, resident = run(True)
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / reps
-    pairs = sum(prefix * count + count * (count + 1) // 2 for prefix, count in plan)
+    score_ms = sum(a.elapsed_time(b) for a, b in timing["score"]) / reps
+    boundary_ms = sum(a.elapsed_time(b) for a, b in timing["boundary"]) / reps
+    pairs = sum(r * min(chunk, prompt - s) + min(chunk, prompt - s) * (min(chunk, prompt - s) + 1) // 2
+                for r, s in zip(resident, starts))
     flop = L * pairs * 2 * HQ * D
-    tflops = flop / (ms * 1e-3) / 1e12
+    tflops = flop / (score_ms * 1e-3) / 1e12
+    evictions = [ev for ev in entry["events"] if "freed" in ev]
+    # Relocation bytes per evicting boundary: every head's kept middle K+V row read and written
+    # and its score read and written (the width is the budget minus the 4608 protected).
+    moved = sum(L * HKV * (ev["after"] - 4608) * (2 * 2 * D * 2 + 4 * 2) for ev in evictions)
+    policy = args.prefill_policy.replace("_2048", "")
     return {
         "metric": "chunked-prefill score tiles, TFLOP/s (one QK^T pass) and % of bf16 MFMA peak",
         "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 1,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"gpt-oss-20b chunked prefill scoring, {L} layers, 79,720-token prompt in 8192-token "
-                               f"chunks, prefix capped at {cap} (512+4096+24064), head_sum, 5% heavy-hitter keys",
+        "config": {"workload": f"gpt-oss-20b chunked prefill, {L} layers, 79,720-token prompt in 8192-token chunks, "
+                               f"{policy}{' 16-token layer-shared blocks' if 'block' in policy else ''}, budget {cap} "
+                               f"(512+4096+24064), 5% heavy-hitter keys",
                    "causal_pairs_per_layer": pairs},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "issued_frac": round(2 * tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": None},
         # Two exponentials per (query head, key) pair (normaliser pass, probability pass).
-        "exp2_T_per_s": round(2 * L * pairs * HQ / (ms * 1e-3) / 1e12, 2),
+        "exp2_T_per_s": round(2 * L * pairs * HQ / (score_ms * 1e-3) / 1e12, 2),
+        "score_ms": round(score_ms, 3),
+        "eviction": {"policy": args.prefill_policy, "boundaries": len(evictions),
+                     "evicted_per_boundary": [ev["before"] - ev["after"] for ev in evictions],
+                     "boundary_ms": round(boundary_ms, 3),
+                     # The last run's relocated bytes over one run's boundary time (selection, block
+                     # scores, relocation and the host wait included).
+                     "relocation_GB_s": round(moved / (boundary_ms * 1e-3) / 1e9, 1) if boundary_ms else None},
     }
 
 
