@@ -6,6 +6,9 @@
 // the budget goes to the highest float64 scores, exact ties keeping the newer
 // position. Positions are unique within a row, so the composite key
 // (ordered score bits, position) is unique and the top-k set is exact.
+#include <algorithm>
+#include <cstdlib>
+
 #include "common.hpp"
 #include "host.hpp"
 
@@ -631,6 +634,18 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
 
 // --------------------------------------------------------- boundary kernels --
 
+// Single-pass relocation (relocate_coop_kernel) geometry and grid barrier.
+// One 1024-thread workgroup per CU at the kernel's register use (4 waves per SIMD); arrivals go
+// to 8 group counters, whose last arrivals bump the counter everyone polls, so no address takes
+// more than 32 atomics per barrier (with all 256 workgroups on one counter the relocation ran at
+// 1.3 TB/s). Polls sleep 20 x 64 cycles between reads.
+constexpr int COOP_THREADS = 1024;
+constexpr int COOP_WAVES = COOP_THREADS / 64;
+constexpr int COOP_GROUPS = 8;
+constexpr int COOP_SLEEP = 20;
+constexpr int COOP_SPIN_LIMIT = 1 << 18;
+
+
 struct BndArgs {
   int layers, kv_heads, head_dim;
   int64_t N, n, budget;
@@ -664,11 +679,14 @@ struct BndArgs {
   int64_t ssl, ssg, sss;
   uint16_t* scratch_kv;
   float* scratch_sc;
+  uint32_t* grid_arrivals;  // single-pass relocation: grid barrier counter (zeroed by prep)
 };
 
 // slots[c] = table[row, c] for c < count, else req_to_token[row, frontier + c - count] (R:428).
 __global__ void prep_slots_kernel(BndArgs a) {
   const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c == 0 && a.grid_arrivals)
+    for (int k = 0; k <= COOP_GROUPS; ++k) a.grid_arrivals[64 * k] = 0;  // the top and group counters
   if (c >= a.N) return;
   a.slots[c] = c < a.row_count ? a.table[int64_t(a.row) * a.table_stride + c]
                                : a.r2t[int64_t(a.row) * a.r2t_stride + a.row_frontier + c - a.row_count];
@@ -884,6 +902,85 @@ __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
   }
 }
 
+// Single-pass relocation for 8 KV heads x 64 dims, launched cooperatively (every workgroup
+// resident at once). Layer by layer, each wave loads its share of the moves (entries j0..j0+per
+// of every head: lane (head lane/8, piece lane%8) carries 16 bytes of K and of V and, on piece 0,
+// the score) into registers, waits for the loads to land, and meets every other workgroup at a
+// grid barrier; then it writes them to their targets. All of a layer's sources are read before
+// any of its targets is written, as the two-kernel path through scratch guarantees (R:455-464),
+// at half its HBM traffic. A layer's stores and the next layer's loads touch different pools, so
+// one barrier per layer suffices. The barrier's wait is bounded: past 2^18 polls (about 0.3 s) a workgroup
+// stops waiting and marks the boundary GSE_BOUNDARY_ERR_RELOCATE, which the host raises.
+
+GSE_DEVICE void grid_barrier(BndArgs& a, uint32_t layer) {
+  // Every load of this workgroup has returned before it arrives.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // Counters 64 words (256 bytes) apart: the top one, then group k's (workgroups k, k + 8, ...).
+    uint32_t* top = a.grid_arrivals;
+    const uint32_t grp = blockIdx.x % COOP_GROUPS;
+    const uint32_t members = (gridDim.x - grp + COOP_GROUPS - 1) / COOP_GROUPS;
+    uint32_t* cnt = a.grid_arrivals + 64 * (1 + grp);
+    const uint32_t before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before + 1 == (layer + 1) * members) __hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t groups = gridDim.x < uint32_t(COOP_GROUPS) ? gridDim.x : uint32_t(COOP_GROUPS);
+    const uint32_t target = (layer + 1) * groups;
+    int spins = 0;
+    while (__hip_atomic_load(top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(COOP_SLEEP);
+      if (++spins > COOP_SPIN_LIMIT) {
+        atomicExch(&a.status->state, int32_t(GSE_BOUNDARY_ERR_RELOCATE));
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+template <int PER>
+__global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) {
+  const gse_boundary_status st = *a.status;
+  if (st.state != GSE_BOUNDARY_EVICTED || st.width <= 0) return;  // the same for every workgroup
+  const int64_t width = st.width;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 3, piece = lane & 7;
+  const int64_t nwaves = int64_t(gridDim.x) * COOP_WAVES;
+  const int64_t per = (width + nwaves - 1) / nwaves;  // <= PER (checked by the host for the budget)
+  const int64_t j0 = (int64_t(blockIdx.x) * COOP_WAVES + (threadIdx.x >> 6)) * per;
+  for (int l = 0; l < a.layers; ++l) {
+    const int lg = l * a.kv_heads + g;
+    auto K = as_global(static_cast<uint16_t*>(a.k_pools[l]));
+    auto V = as_global(static_cast<uint16_t*>(a.v_pools[l]));
+    const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
+    float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
+    uint4 kv[PER][2];
+    float sc[PER];
+    int64_t dst[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int64_t j = j0 + r;
+      dst[r] = -1;
+      if (r < per && j < width) {
+        const int64_t src = a.slots[a.middle[int64_t(lg) * a.budget + j]];
+        dst[r] = a.targets[j];
+        kv[r][0] = gload16(K + src * a.kv_ss + off);
+        kv[r][1] = gload16(V + src * a.kv_ss + off);
+        sc[r] = srow[src * a.sss];
+      }
+    }
+    grid_barrier(a, uint32_t(l));
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      if (dst[r] < 0) continue;
+      gstore16(K + dst[r] * a.kv_ss + off, kv[r][0]);
+      gstore16(V + dst[r] * a.kv_ss + off, kv[r][1]);
+      if (piece == 0) srow[dst[r] * a.sss] = sc[r];
+    }
+  }
+}
+
 // pos_new[l, g, i] = pos(l, g, prot_cols[i]) for the protected prefix of every head row.
 __global__ __launch_bounds__(256) void protected_pos_kernel(BndArgs a) {
   const gse_boundary_status st = *a.status;
@@ -1079,7 +1176,7 @@ namespace {
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 struct BndLayout {
-  int64_t slots, keys, posw, prot, middle, prot_cols, targets, skv, ssc, bypos, bscore, colscore, total;
+  int64_t slots, keys, posw, prot, middle, prot_cols, targets, skv, ssc, bypos, bscore, colscore, arrivals, total;
 };
 
 bool block_policy(int policy) { return policy == GSE_POLICY_BLOCK_SUM || policy == GSE_POLICY_BLOCK_MAX; }
@@ -1093,6 +1190,7 @@ BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t 
   const int64_t nblocks = blk && block > 0 ? (n + block - 1) / block : 0;
   BndLayout L;
   int64_t o = 0;
+  L.arrivals = o; o += 256 * (1 + COOP_GROUPS);
   L.bypos = o; o += blk ? align256(LG * n * 4) : 0;
   L.bscore = o; o += blk ? align256(LG * nblocks * 8) : 0;
   L.colscore = o; o += blk ? align256(LG * N * 8) : 0;
@@ -1107,6 +1205,36 @@ BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t 
   L.ssc = o; o += align256(LG * budget * 4);
   L.total = o;
   return L;
+}
+
+// Grid of the single-pass relocation: every workgroup the device can hold at once (cached per
+// device), and the moves per wave for a width of up to `budget`; no plan (0 blocks) when the
+// device lacks cooperative launch or a layer's moves do not fit in registers (8 per wave).
+void coop_plan(int64_t budget, int* blocks, int* per) {
+  static int cached[64] = {0};  // resident workgroups per device, -1 = no cooperative launch
+  *blocks = *per = 0;
+  // GSE_RELOCATE_SCRATCH=1 keeps the two-kernel path through scratch (tests run both).
+  const char* force = getenv("GSE_RELOCATE_SCRATCH");
+  if (force && force[0] == '1') return;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
+  if (!cached[dev]) {
+    int coop = 0, cus = 0, per_cu = 0;
+    const bool ok = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess && coop &&
+                    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                    hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &per_cu, reinterpret_cast<const void*>(&relocate_coop_kernel<8>), COOP_THREADS, 0) ==
+                        hipSuccess &&
+                    cus > 0 && per_cu > 0;
+    cached[dev] = ok ? cus * per_cu : -1;
+  }
+  if (cached[dev] <= 0 || budget <= 0) return;
+  const int64_t waves = int64_t(cached[dev]) * COOP_WAVES;
+  const int64_t need = (budget + waves - 1) / waves;
+  if (need > 8) return;
+  // One move per wave at least: small widths use fewer workgroups.
+  *blocks = int(std::min<int64_t>(cached[dev], (budget + COOP_WAVES - 1) / COOP_WAVES));
+  *per = int((budget + int64_t(*blocks) * COOP_WAVES - 1) / (int64_t(*blocks) * COOP_WAVES));
 }
 
 size_t select_lds_bytes(int nwords) {
@@ -1240,6 +1368,7 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   b.sss = scores_stride_s;
   b.scratch_kv = reinterpret_cast<uint16_t*>(ws + L.skv);
   b.scratch_sc = reinterpret_cast<float*>(ws + L.ssc);
+  b.grid_arrivals = reinterpret_cast<uint32_t*>(ws + L.arrivals);
 
   hipLaunchKernelGGL(prep_slots_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, s, b);
   if (int rc = gse_launch_check("boundary prep")) return rc;
@@ -1324,7 +1453,16 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   hipLaunchKernelGGL(columns_kernel, dim3(1), dim3(SEL_THREADS), col_lds, s, b);
   if (int rc = gse_launch_check("boundary columns")) return rc;
 
-  if (kv_heads == 8 && head_dim == 64) {
+  int coop_blocks = 0, coop_per = 0;
+  if (kv_heads == 8 && head_dim == 64) coop_plan(budget, &coop_blocks, &coop_per);
+  if (coop_blocks > 0) {
+    void* args[] = {&b};
+    const void* fn = coop_per <= 4 ? reinterpret_cast<const void*>(&relocate_coop_kernel<4>)
+                                   : reinterpret_cast<const void*>(&relocate_coop_kernel<8>);
+    if (hipLaunchCooperativeKernel(fn, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), args, 0, s) != hipSuccess)
+      return gse_fail(GSE_ELAUNCH, "boundary: cooperative relocation launch failed");
+    if (int rc = gse_launch_check("boundary relocate")) return rc;
+  } else if (kv_heads == 8 && head_dim == 64) {
     const dim3 rgrid(unsigned((budget + 4 * ROWS_PER_WAVE - 1) / (4 * ROWS_PER_WAVE)), unsigned(layers));
     hipLaunchKernelGGL(relocate_rows_kernel<0>, rgrid, dim3(256), 0, s, b);
     if (int rc = gse_launch_check("boundary gather")) return rc;

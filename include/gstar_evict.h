@@ -63,7 +63,9 @@ enum {
   GSE_BOUNDARY_DEFERRED = 2,       /* protected count > budget (R:390-391, R:438-441)       */
   GSE_BOUNDARY_ERR_HEADS = 3,      /* heads protect different counts (R:388-389)             */
   GSE_BOUNDARY_ERR_SWA = 4,        /* a leftover slot still holds a sliding-window entry (R:477-479) */
-  GSE_BOUNDARY_ERR_PACKED = 5      /* packed ownership overlaps the sliding-window region (R:487-489) */
+  GSE_BOUNDARY_ERR_PACKED = 5,     /* packed ownership overlaps the sliding-window region (R:487-489) */
+  GSE_BOUNDARY_ERR_RELOCATE = 6    /* the single-pass relocation's grid barrier timed out (its
+                                      workgroups were not all resident); no reference counterpart */
 };
 
 typedef struct {
