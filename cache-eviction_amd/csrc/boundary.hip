@@ -105,6 +105,9 @@ struct ColSrc {
   const int32_t* slots;
   const double* random_scores;
   int64_t seed;
+  // Table-score policies: the columns' table scores per (layer, head) row, [LG, N] (written by
+  // table_columns_kernel from each slot's score row, read once for all of its heads).
+  const float* column_scores;
 };
 
 struct SelArgs {
@@ -208,8 +211,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
                  a.src.policy == GSE_POLICY_BLOCK_MAX) {
         sc = a.src.random_scores[int64_t(lg) * N + c];
       } else {
-        sc = double(a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg +
-                                       int64_t(a.src.slots[c]) * a.src.sss]);
+        sc = double(a.src.column_scores[int64_t(lg) * N + c]);
       }
     }
     keys[c] = ordered_f64(sc);
@@ -357,7 +359,7 @@ GSE_DEVICE uint64_t col_key64(const SelArgs& a, int l, int g, int lg, int64_t c,
   if (a.src.policy == GSE_POLICY_RANDOM || a.src.policy == GSE_POLICY_BLOCK_SUM || a.src.policy == GSE_POLICY_BLOCK_MAX)
     return ordered_f64(a.src.random_scores[int64_t(lg) * a.n_cols + c]);
   if (a.src.policy == GSE_POLICY_PREFIX_SLIDING) return uint64_t(ordered_f32(0.f)) << 32;
-  const float sc = a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg + int64_t(a.src.slots[c]) * a.src.sss];
+  const float sc = a.src.column_scores[int64_t(lg) * a.n_cols + c];
   return uint64_t(ordered_f32(sc)) << 32;
 }
 
@@ -423,15 +425,12 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
     load_pos(k0, pb);
     float sc[BATCH];
     if (table_scores) {
-      int32_t sl[BATCH];
+      const float* crow = a.src.column_scores + int64_t(lg) * N;
 #pragma unroll
       for (int u = 0; u < BATCH; ++u) {
         const int c = col(k0 + u);
-        sl[u] = a.src.slots[c < N ? c : N - 1];
+        sc[u] = crow[c < N ? c : N - 1];
       }
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u)
-        sc[u] = a.src.table_scores[int64_t(l) * a.src.ssl + int64_t(g) * a.src.ssg + int64_t(sl[u]) * a.src.sss];
     }
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
@@ -993,6 +992,21 @@ __global__ __launch_bounds__(256) void protected_pos_kernel(BndArgs a) {
   }
 }
 
+// ----------------------------------------------------- table column scores --
+//
+// The table-score policies rank each (layer, head) row by its columns' scores. A slot keeps its
+// heads' scores together (one 32-byte row at 8 heads), so one thread per (layer, column) reads
+// the row once and writes each head's score into that head's contiguous column array, instead of
+// every head's selection gathering the same row for 4 of its bytes. Grid (ceil(N / 256), layers).
+__global__ void table_columns_kernel(const float* scores, int64_t ssl, int64_t ssg, int64_t sss,
+                                     const int32_t* slots, int kv_heads, int64_t N, float* out) {
+  const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int l = blockIdx.y;
+  if (c >= N) return;
+  const float* row = scores + int64_t(l) * ssl + int64_t(slots[c]) * sss;
+  for (int g = 0; g < kv_heads; ++g) out[(int64_t(l) * kv_heads + g) * N + c] = row[int64_t(g) * ssg];
+}
+
 // ------------------------------------------------------ block policy scores --
 //
 // block_sum_2048 / block_max_2048 rank whole blocks of `block` consecutive positions. A
@@ -1176,7 +1190,8 @@ namespace {
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 struct BndLayout {
-  int64_t slots, keys, posw, prot, middle, prot_cols, targets, skv, ssc, bypos, bscore, colscore, arrivals, total;
+  int64_t slots, keys, posw, prot, middle, prot_cols, targets, skv, ssc, bypos, bscore, colscore, col32, arrivals,
+      total;
 };
 
 bool block_policy(int policy) { return policy == GSE_POLICY_BLOCK_SUM || policy == GSE_POLICY_BLOCK_MAX; }
@@ -1191,6 +1206,8 @@ BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t 
   BndLayout L;
   int64_t o = 0;
   L.arrivals = o; o += 256 * (1 + COOP_GROUPS);
+  const bool table = policy == GSE_POLICY_HEAD_SUM || policy == GSE_POLICY_HEAD_MAX_SUM;
+  L.col32 = o; o += table ? align256(LG * N * 4) : 0;
   L.bypos = o; o += blk ? align256(LG * n * 4) : 0;
   L.bscore = o; o += blk ? align256(LG * nblocks * 8) : 0;
   L.colscore = o; o += blk ? align256(LG * N * 8) : 0;
@@ -1408,6 +1425,13 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
     if (int rc = gse_launch_check("boundary block columns")) return rc;
     f64_scores = k.colscore;
   }
+  float* column_scores = nullptr;
+  if (policy == GSE_POLICY_HEAD_SUM || policy == GSE_POLICY_HEAD_MAX_SUM) {
+    column_scores = reinterpret_cast<float*>(ws + L.col32);
+    hipLaunchKernelGGL(table_columns_kernel, dim3(unsigned((N + 255) / 256), unsigned(layers)), dim3(256), 0, s, scores,
+                       scores_stride_l, scores_stride_g, scores_stride_s, b.slots, kv_heads, N, column_scores);
+    if (int rc = gse_launch_check("boundary table columns")) return rc;
+  }
 
   SelArgs a = {};
   a.src.pos_old = pos_old;
@@ -1422,6 +1446,7 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   a.src.slots = b.slots;
   a.src.random_scores = f64_scores;
   a.src.seed = seed;
+  a.src.column_scores = column_scores;
   a.layers = layers;
   a.kv_heads = kv_heads;
   a.n_cols = N;

@@ -125,7 +125,9 @@ int64_t gse_decode_workspace_bytes(int bs, int q_heads, int head_dim);
  * full (a count above queue_cap records dropped steps) and before the row's list changes
  * other than by appending (boundaries). Shapes: q_heads = 8 * kv_heads, kv_heads <= 8,
  * head_dim = 64. The attention kernel runs one workgroup per CU over an equal share of
- * the batch's keys; fixed grid, no host reads: capturable in a HIP graph.
+ * the batch's keys; fixed grid, no host reads: capturable in a HIP graph. rows[b] must
+ * index mode_by_row and the queue buffers (as SGLang's req_pool_indices index
+ * req_to_token): the kernels do not check it.
  */
 int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
