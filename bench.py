@@ -53,6 +53,8 @@ def parse(argv=None):
     p.add_argument("--kernel-reps", type=int, default=20, help="launches timed per layer for the roofline")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--eager", action="store_true", help="score each step eagerly (second K pass per step)")
+    p.add_argument("--decode-latency", action="store_true",
+                   help="bs=1 decode layer latency at 8K/16K/32K resident (the reference's published shape)")
     p.add_argument("--prefill-policy", default="block_sum_2048",
                    help="eviction policy of the --prefill workload (block policies: 16-token layer-shared blocks)")
     p.add_argument("--prefill", action="store_true",
@@ -526,6 +528,110 @@ def prefill_bench(args, torch, ge):
     }
 
 
+def decode_latency_bench(args, torch, ge):
+    """One full-attention decode layer at bs=1 (64 q heads, 8 KV heads, d=64, bf16, 16-token pages
+    in random order), at 8192, 16384 and 32768 resident keys: the shape of the reference's own
+    published timings (SGLang decode attention alone, then with its score kernel). Per size, with
+    HIP events over 200 calls replayed from HIP graphs of 32 calls (after 20 warmups):
+      attention  - a row without a score policy (mode 0): attention only;
+      queued     - head_sum: attention, the step queued, plus the flush of a full 64-step queue
+                   for this layer amortised over its 64 steps (timed separately);
+      eager      - head_sum with the score added in the same call (a second pass over K).
+    """
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    sizes = (8192, 16384, 32768)
+    slots = max(sizes) + 64
+    k = torch.randn((slots + 1, HKV, D), device=dev, dtype=torch.bfloat16, generator=g)
+    v = torch.randn((slots + 1, HKV, D), device=dev, dtype=torch.bfloat16, generator=g)
+    pool = SimpleNamespace(layers_mapping={0: (0, False)}, get_key_buffer=lambda l: k, get_value_buffer=lambda l: v)
+    width = slots + 256
+    backend = SimpleNamespace(token_to_kv_pool=pool, max_kv_splits=8,
+                              req_to_token_pool=SimpleNamespace(req_to_token=torch.zeros((2, width), dtype=torch.int32,
+                                                                                         device=dev)),
+                              kv_indptr=torch.zeros(3, dtype=torch.int32, device=dev))
+    pages = torch.randperm(slots // PAGE, device=dev, generator=g)
+    order = (pages[:, None] * PAGE + torch.arange(PAGE, device=dev)[None]).reshape(-1) + 1
+    q = torch.randn((1, HQ, D), device=dev, dtype=torch.bfloat16, generator=g)
+    sinks = torch.randn(HQ, device=dev, dtype=torch.bfloat16, generator=g)
+    o = torch.empty((1, HQ, D), device=dev, dtype=torch.bfloat16)
+    lay = SimpleNamespace(sliding_window_size=-1, tp_q_head_num=HQ, tp_k_head_num=HKV, qk_head_dim=D, layer_id=0,
+                          scaling=D ** -0.5)
+    rows = torch.tensor([1], device=dev)
+    reps, warm = 200, 20
+
+    def timed(fn, n):
+        """Per-call µs of ``fn`` replayed from a HIP graph of 32 calls (the GPU's time, without the
+        Python launch path, which is slower than a bs=1 layer)."""
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(32):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        replays = max(1, n // 32)
+        start.record()
+        for _ in range(replays):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return 1000 * start.elapsed_time(end) / (replays * 32)
+
+    results = []
+    for n in sizes:
+        out = {"resident": n}
+        for mode_name, score_mode, policy_mode in (("attention", "queue", 0), ("queued", "queue", 1),
+                                                     ("eager", "eager", 1)):
+            ge.STATE = None
+            st = ge.state(backend)
+            st.score_mode = score_mode
+            st.mode[1] = policy_mode
+            st.req_to_token[1, :n] = order[:n].int()
+            kv_indices = torch.zeros(n, dtype=torch.int32, device=dev)
+            ge.fill(backend, 1, torch.tensor([n], device=dev), rows, kv_indices)
+            backend.forward_metadata = SimpleNamespace(kv_indptr=backend.kv_indptr[:2], kv_indices=kv_indices)
+            fb = SimpleNamespace(out_cache_loc=order[n - 1:n], req_pool_indices=rows, seq_lens_cpu=[n])
+
+            def step():
+                # Past the queue's capacity the merge only counts the step (no entry is written):
+                # the queue's flush is timed below.
+                ge.decode(backend, q.view(1, -1), lay, fb, sinks, o.view(1, -1))
+
+            us = timed(step, reps)
+            if mode_name == "queued":
+                # A full queue: 64 steps of this layer, then one flush (the step loop above reset it).
+                st.qcount.fill_(st.queue_cap)
+                st.qlim[:, 1] = n
+                st.qnorm[:, 1] = 10.0
+                st.qq[:, 1] = q.view(1, 1, HQ, D).expand(-1, st.queue_cap, -1, -1)
+
+                def flush():
+                    st.qcount[:, 1] = st.queue_cap
+                    st.queued[1] = st.queue_cap
+                    ge.flush(st, [1])
+
+                flush_us = timed(flush, 20)
+                out["queued_flush_us"] = round(flush_us, 1)
+                us += flush_us / st.queue_cap
+            out[f"{mode_name}_us"] = round(us, 2)
+        out["attention_GB_s"] = round((2052 * n + 16512) / (out["attention_us"] * 1e-6) / 1e9, 1)
+        results.append(out)
+    return {
+        "metric": "bs=1 decode layer latency (gpt-oss-20b full-attention shape), us",
+        "value": results[0]["queued_us"], "unit": "us", "n_gpus": 1, "steps": reps, "warmup": warm,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "one full-attention decode layer, bs=1, 64 q heads, 8 KV heads, d=64, bf16, "
+                               "16-token pages in random order, head_sum, resident 8192 / 16384 / 32768"},
+        "sizes": results,
+        "reference_gb10": {"8192": {"attention_us": 58.9, "with_scores_us": 83.9},
+                           "16384": {"attention_us": 150.0, "with_scores_us": 192.9}},
+    }
+
+
 def replay_bench(args, torch, ge):
     """Static replay's layer difference over a 79,720-token prompt in 2048-token chunks with
     2048 positions retained per KV head after each boundary: per chunk, the first full layer's
@@ -624,6 +730,9 @@ def main():
         return
     if args.replay:
         print(json.dumps(replay_bench(args, torch, ge)), flush=True)
+        return
+    if args.decode_latency:
+        print(json.dumps(decode_latency_bench(args, torch, ge)), flush=True)
         return
     w = Workload(args, torch, ge)
     for _ in range(args.warmup):

@@ -282,11 +282,14 @@ struct MergeArgs {
   int bs, q_heads, nparts;  // nparts = P, the fused kernel's workgroup count
 };
 
-// Grid (bs, q_heads / MERGE_HEADS), MERGE_THREADS threads: thread (head 8*y + t/16, dims
-// [4*(t%16), +4)) merges the partials of its head with the sink:
+// Grid (bs, q_heads / MERGE_HEADS), MERGE_THREADS * SPLIT threads: thread (head 8*y + t/16,
+// dims [4*(t%16), +4)) of partial group k = t / MERGE_THREADS merges every SPLIT-th batch of the
+// sequence's partials of its head, group 0 starting from the sink:
 //   o = sum_w 2^(m_w - M) o_w / (2^(sink - M) + sum_w 2^(m_w - M) l_w), M the maximum,
 // MERGE_BATCH partials at a time with all their loads in flight together (a partial past
-// the range is read again with weight 0), one rescale of the running sums per batch.
+// the range is read again with weight 0), one rescale of the running sums per batch; with
+// SPLIT > 1 (few sequences, each spread over many workgroups) group 0 then folds the other
+// groups' (m, l, o) from LDS, so a sequence's partials cost ceil(count / (8 * SPLIT)) rounds.
 // A sequence's head groups run in separate workgroups, so its queue count is advanced by the
 // last of them to finish: each adds one arrival ticket (bit 24 up) to the count word after it
 // has read the count, and the one that sees every other ticket there removes the tickets and
@@ -294,13 +297,19 @@ struct MergeArgs {
 constexpr int MERGE_HEADS = 8;
 constexpr int MERGE_THREADS = MERGE_HEADS * 16;
 constexpr int MERGE_BATCH = 8;
+constexpr int MERGE_SPLIT = 8;  // partial groups for batches of fewer sequences than workgroups / 8
 constexpr int32_t QUEUE_TICKET = 1 << 24;
 constexpr int32_t QUEUE_COUNT_MASK = QUEUE_TICKET - 1;
 
-__global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(MergeArgs a) {
+template <int SPLIT>
+__global__ __launch_bounds__(MERGE_THREADS * SPLIT) void decode_merge_kernel(MergeArgs a) {
+  __shared__ float red_m[SPLIT][MERGE_THREADS], red_l[SPLIT][MERGE_THREADS];
+  __shared__ f32x4_t red_o[SPLIT][MERGE_THREADS];
   const int b = blockIdx.x;
-  const int h = blockIdx.y * MERGE_HEADS + (threadIdx.x >> 4);
-  const int j = threadIdx.x & 15;
+  const int t = threadIdx.x % MERGE_THREADS;
+  const int grp = threadIdx.x / MERGE_THREADS;
+  const int h = blockIdx.y * MERGE_HEADS + (t >> 4);
+  const int j = t & 15;
   // Independent loads first: the queue slot (row -> mode, count) and the partial range
   // (indptr) are two short chains issued together.
   int64_t row = 0;
@@ -323,10 +332,10 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(MergeArgs a
     wf = start / C;
     wl = (end - 1) / C;
   }
-  float mx = load_float_dyn(a.sinks, a.sinks_dtype, hh) * kLog2e;
-  float lsum = 1.f;
+  float mx = grp == 0 ? load_float_dyn(a.sinks, a.sinks_dtype, hh) * kLog2e : -INFINITY;
+  float lsum = grp == 0 ? 1.f : 0.f;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int w0 = wf; w0 <= wl; w0 += MERGE_BATCH) {
+  for (int w0 = wf + grp * MERGE_BATCH; w0 <= wl; w0 += SPLIT * MERGE_BATCH) {
     float pm[MERGE_BATCH], pl[MERGE_BATCH];
     f32x4_t po[MERGE_BATCH];
 #pragma unroll
@@ -340,7 +349,7 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(MergeArgs a
     float m_new = mx;
 #pragma unroll
     for (int k = 0; k < MERGE_BATCH; ++k) m_new = fmaxf(m_new, pm[k]);
-    const float so = fast_exp2(mx - m_new);
+    const float so = fast_exp2(mx - m_new);  // 0 for a group still at -inf
     lsum *= so;
     acc = acc * so;
 #pragma unroll
@@ -351,7 +360,25 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(MergeArgs a
     }
     mx = m_new;
   }
-  if (live) {
+  if (SPLIT > 1) {
+    red_m[grp][t] = mx;
+    red_l[grp][t] = lsum;
+    red_o[grp][t] = acc;
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+      for (int k = 1; k < SPLIT; ++k) mx = fmaxf(mx, red_m[k][t]);  // group 0's sink keeps mx finite
+      lsum = 0.f;
+      acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < SPLIT; ++k) {
+        const float sk = fast_exp2(red_m[k][t] - mx);
+        lsum += red_l[k][t] * sk;
+        acc += red_o[k][t] * sk;
+      }
+    }
+  }
+  if (live && grp == 0) {
     const float inv = 1.f / lsum;
     uint2 out;
     out.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
@@ -516,9 +543,14 @@ int check_decode_shape(int q_heads, int kv_heads, int head_dim) {
   return GSE_OK;
 }
 
-// One score-only pass over K (splits of 1024 keys; max_len bounds every sequence's length).
+// One score-only pass over K; max_len bounds every sequence's length. A workgroup walks its
+// chunk 16 keys per dependent step, so the chunk (64..1024 keys) is sized to give about four
+// workgroups per CU over the batch.
 int score_pass(ScoreArgs s, int indices_dtype, int bs, int max_len, hipStream_t stream) {
-  s.chunk = 1024;
+  const int64_t target = 4 * int64_t(fused_workgroups());
+  int64_t chunk = (int64_t(max_len) * bs + target - 1) / target;
+  chunk = (chunk + 63) / 64 * 64;
+  s.chunk = int(chunk < 64 ? 64 : (chunk > 1024 ? 1024 : chunk));
   const int splits = (max_len + s.chunk - 1) / s.chunk;
   if (splits <= 0 || bs <= 0) return GSE_OK;
   const dim3 grid{static_cast<uint32_t>(splits), static_cast<uint32_t>(bs)}, block{FUSED_THREADS};
@@ -619,7 +651,10 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   m.q_heads = q_heads;
   m.nparts = P;
   const dim3 mgrid(static_cast<uint32_t>(bs), static_cast<uint32_t>((q_heads + MERGE_HEADS - 1) / MERGE_HEADS));
-  hipLaunchKernelGGL(decode_merge_kernel, mgrid, dim3(MERGE_THREADS), 0, s, m);
+  if (int64_t(bs) * MERGE_SPLIT < P)  // a sequence spans more than 8 workgroups on average
+    hipLaunchKernelGGL(decode_merge_kernel<MERGE_SPLIT>, mgrid, dim3(MERGE_THREADS * MERGE_SPLIT), 0, s, m);
+  else
+    hipLaunchKernelGGL(decode_merge_kernel<1>, mgrid, dim3(MERGE_THREADS), 0, s, m);
   if ((rc = gse_launch_check("decode_merge"))) return rc;
 
   if (score_mode == GSE_SCORE_EAGER) {

@@ -287,3 +287,31 @@ def test_merge_of_empty_short_and_long_sequences_over_a_reused_workspace():
             np.testing.assert_allclose(st.qnorm[index, row, 0].cpu().numpy(), want_norm, rtol=1e-5, atol=1e-4)
         assert torch.equal(st.qq[index, rows, 0], q)
         ge.STATE = None
+
+
+@pytest.mark.parametrize("bs", [40, 3])
+def test_merge_paths_for_many_and_few_sequences(bs):
+    """The merge folds a sequence's partials in one group when there are at least 32 sequences
+    (about 8 workgroups each) and in 8 groups combined through LDS below that (one sequence spread
+    over up to 256 workgroups): both against the oracle, outputs and queued normalisers."""
+    g = np.random.default_rng(bs)
+    lengths = [int(x) for x in g.integers(1, 400 if bs > 8 else 6000, size=bs)]
+    b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths, seed=30 + bs, slots=40000)
+    st.score_mode = "queue"
+    st.mode[:] = 1
+    b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=perm)
+    fb = SimpleNamespace(out_cache_loc=torch.zeros(bs, dtype=torch.int64, device="cuda"), req_pool_indices=rows,
+                         seq_lens_cpu=torch.tensor(lengths))
+    o = torch.empty_like(q)
+    assert ge.decode(b, q.reshape(bs, -1), layer(1), fb, sinks, o.reshape(bs, -1))
+    keys = b.token_to_kv_pool.get_key_buffer(1).float().cpu().numpy()
+    values = b.token_to_kv_pool.get_value_buffer(1).float().cpu().numpy()
+    ip, pm, sn = indptr.cpu().numpy(), perm.cpu().numpy(), sinks.float().cpu().numpy()
+    got = o.float().cpu().numpy()
+    index = st.index[1]
+    norms = st.qnorm[index, 1:bs + 1, 0].cpu().numpy()
+    for i in range(bs):
+        want_o, want_norm = O.decode_attention(q[i].float().cpu().numpy(), keys, values, pm[ip[i]:ip[i + 1]], sn, 0.125)
+        np.testing.assert_allclose(got[i], want_o, rtol=2e-2, atol=2e-2)
+        np.testing.assert_allclose(norms[i], want_norm, rtol=1e-5, atol=1e-4)
+    assert st.qcount[index, 1:bs + 1].tolist() == [1] * bs
