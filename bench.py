@@ -222,6 +222,7 @@ class Workload:
         self.boundaries = 0
         self.started = []  # (sequence, n) of the boundaries queued in timed steps
         self.unaccounted = None  # sequence lengths of the last step, until its boundaries finish
+        self.boundary_ms = []  # (ranking, compaction) device ms of each timed evicting boundary
         self.resident_hist = []
 
     def account_boundaries(self):
@@ -233,6 +234,7 @@ class Workload:
                 width = ev["after"] - (a.prefix + a.recent)
                 self.bytes += boundary_bytes(ev["before"], max(width, 0), ev["after"], ev["freed"], a.layers)
                 self.boundaries += 1
+                self.boundary_ms.append((ev["ranking_ms"], ev["compaction_ms"]))
         self.started = []
 
     def resident(self, i):
@@ -770,6 +772,11 @@ def main():
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": per_launch, "avg_launch_us": round(avg_us, 2)},
         "step_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+        # Medians over the timed evicting boundaries, device time from the boundary's events:
+        # ranking = score flush + selection + relocation, compaction = leftover scores, repack.
+        "boundary_median_ms": {
+            "ranking": round(statistics.median(r for r, _ in w.boundary_ms), 3) if w.boundary_ms else None,
+            "compaction": round(statistics.median(c for _, c in w.boundary_ms), 3) if w.boundary_ms else None},
         # Everything a step adds to its decode attention (score flush, selection, compaction, CSR
         # fill, host waits), relative to the attention launches alone.
         "evict_overhead_vs_attention": round((1000 * ms_step - args.layers * avg_us) / (args.layers * avg_us), 4),

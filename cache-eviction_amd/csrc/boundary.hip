@@ -386,6 +386,96 @@ GSE_DEVICE int cmp96(uint32_t hi, uint32_t lo, uint32_t pos, uint32_t th, uint32
   return cmp_top(pos, tp, fixed - 8);
 }
 
+// Sets bit p of the LDS bitmap for the lanes with `act`. Lanes whose positions share a 32-bit
+// word pool their bits first (positions of neighbouring columns mostly do): up to 4 rounds, each
+// taking the lowest active lane's word, one atomic per round; lanes left after that OR alone.
+GSE_DEVICE void wave_set_bit(uint32_t* words, int32_t p, bool act) {
+  const uint32_t w = uint32_t(p) >> 5, bit = 1u << (uint32_t(p) & 31u);
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int round = 0; round < 4; ++round) {
+    const uint64_t live = __ballot(act);
+    if (!live) return;
+    const int leader = __ffsll(static_cast<unsigned long long>(live)) - 1;
+    const uint32_t lw = __shfl(w, leader, 64);
+    const bool mine = act && w == lw;
+    uint32_t v = mine ? bit : 0u;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v |= __shfl_xor(v, o, 64);
+    if (lane == leader) atomicOr(&words[lw], v);
+    act = act && !mine;
+  }
+  if (act) atomicOr(&words[w], bit);
+}
+
+// wpre[w] = set bits of words[0, w) (one block scan over contiguous runs of words); the rank
+// of a set position p is then wpre[p / 32] + the set bits below it in its word.
+GSE_DEVICE void bitmap_word_prefix(const uint32_t* words, int nwords, int* wpre, int* tmp) {
+  const int per = (nwords + SEL_THREADS - 1) / SEL_THREADS;
+  const int w0 = threadIdx.x * per, w1 = min(nwords, w0 + per);
+  int cnt = 0;
+  for (int w = w0; w < w1; ++w) cnt += __popc(words[w]);
+  int total;
+  int run = block_exclusive_scan<SEL_THREADS>(cnt, tmp, &total);
+  for (int w = w0; w < w1; ++w) {
+    wpre[w] = run;
+    run += __popc(words[w]);
+  }
+  __syncthreads();
+}
+
+GSE_DEVICE int word_rank(const uint32_t* words, const int* wpre, int32_t p) {
+  const int w = p >> 5;
+  return wpre[w] + __popc(words[w] & ((1u << (p & 31)) - 1u));
+}
+
+// The protected columns of head (0, 0) ranked by position (the new table's protected part),
+// by one extra workgroup of the selection grid, beside the per-head selections.
+GSE_DEVICE void protected_columns(const SelArgs& a, uint32_t* words, int* wpre, int* tmp) {
+  constexpr int KPT = SEL_LDS_KEYS / SEL_THREADS;
+  constexpr int BATCH = 17;
+  const int N = int(a.n_cols);
+  const int cnt = int(a.src.count);
+  const int32_t* prow = (a.src.pos_old && cnt > 0) ? a.src.pos_old : nullptr;  // row (0, 0)
+  auto col = [&](int k) { return int(threadIdx.x) + k * SEL_THREADS; };
+  auto load_pos = [&](int k0, int32_t* pb) {
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = col(k0 + u);
+      const int32_t v = prow ? prow[c < cnt ? c : cnt - 1] : 0;
+      pb[u] = c < cnt ? v : int32_t(a.src.frontier + c - cnt);
+    }
+  };
+  for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
+  __syncthreads();
+  int nprot = 0;
+  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
+    int32_t pb[BATCH];
+    load_pos(k0, pb);
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = col(k0 + u);
+      const bool prot = c < N && is_protected(a, pb[u]);
+      nprot += prot;
+      wave_set_bit(words, pb[u], prot && pb[u] < a.n);
+    }
+  }
+  const int P = block_sum(nprot, tmp);
+  if (P > a.budget) return;  // deferred
+  bitmap_word_prefix(words, a.nwords, wpre, tmp);
+  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
+    int32_t pb[BATCH];
+    load_pos(k0, pb);
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = col(k0 + u);
+      if (c >= N || !is_protected(a, pb[u]) || pb[u] >= a.n) continue;
+      const int r = word_rank(words, wpre, pb[u]);
+      if (r < P) a.prot_cols[r] = c;
+    }
+  }
+}
+
 __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
   constexpr int KPT = SEL_LDS_KEYS / SEL_THREADS;  // columns per thread: c = tid + k * SEL_THREADS
   constexpr int BATCH = 17;                         // columns whose loads are issued together
@@ -397,6 +487,10 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
   __shared__ uint32_t kbits[SEL_LDS_KEYS / 32];  // kept-middle flag per column
   __shared__ uint32_t redu[2][SEL_THREADS / 64];
 
+  if (int(blockIdx.x) == a.layers * a.kv_heads) {  // the extra workgroup: protected columns
+    protected_columns(a, keys, reinterpret_cast<int*>(keys + a.nwords), tmp);
+    return;
+  }
   const int lg = blockIdx.x;
   const int l = lg / a.kv_heads, g = lg % a.kv_heads;
   const int N = int(a.n_cols);
@@ -547,34 +641,41 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
     }
   }
 
-  // Phase 3a: kept-middle flags (unprotected and at or above the threshold prefix).
-  for (int w = threadIdx.x; w < (N + 31) / 32; w += SEL_THREADS) kbits[w] = 0;
-  __syncthreads();
-  if (k > 0) {
-    for (int c = threadIdx.x; c < N; c += SEL_THREADS) {
+  // Phase 3a: kept-middle flags (unprotected and at or above the threshold prefix). Column
+  // tid + k * SEL_THREADS puts a wave on 64 consecutive columns: one ballot per wave writes
+  // their two flag words (every word is written, so no clearing is needed).
+  for (int kk = 0; kk < KPT; ++kk) {
+    const int c = col(kk);
+    bool kept = false;
+    if (k > 0 && c < N) {
       const uint32_t hi = keys[c];
-      if (hi == 0) continue;
-      bool kept = take_all;
-      if (!kept) {
-        const int ch = cmp96(hi, 0, 0, th, tl, tp, fixed < 4 ? fixed : 4);
-        if (ch != 0 || fixed <= 4) {
-          kept = ch >= 0;
-        } else {
-          const int32_t p = col_pos(a, lg, c);
-          const uint32_t lo = f64 ? uint32_t(col_key64(a, l, g, lg, c, p)) : 0u;
-          kept = cmp96(hi, lo, uint32_t(p), th, tl, tp, fixed) >= 0;
+      if (hi != 0) {
+        kept = take_all;
+        if (!kept) {
+          const int ch = cmp96(hi, 0, 0, th, tl, tp, fixed < 4 ? fixed : 4);
+          if (ch != 0 || fixed <= 4) {
+            kept = ch >= 0;
+          } else {
+            const int32_t p = col_pos(a, lg, c);
+            const uint32_t lo = f64 ? uint32_t(col_key64(a, l, g, lg, c, p)) : 0u;
+            kept = cmp96(hi, lo, uint32_t(p), th, tl, tp, fixed) >= 0;
+          }
         }
       }
-      if (kept) atomicOr(&kbits[c >> 5], 1u << (c & 31));
+    }
+    const uint64_t m = __ballot(kept);
+    if (lane == 0) {
+      kbits[c >> 5] = uint32_t(m);
+      kbits[(c >> 5) + 1] = uint32_t(m >> 32);
     }
   }
   __syncthreads();
   if (P > a.budget) return;  // deferred: outputs untouched
 
-  // Phase 3b: kept middle columns ranked by position (bitmap over positions in the keys
-  // region, which is free now).
+  // Phase 3b: kept middle columns ranked by position (bitmap over positions and its per-word
+  // prefix counts in the keys region, which is free now).
   uint32_t* words = keys;
-  int* blockpre = reinterpret_cast<int*>(keys + a.nwords);
+  int* wpre = reinterpret_cast<int*>(keys + a.nwords);
   for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
   __syncthreads();
   for (int k0 = 0; k0 < KPT; k0 += BATCH) {
@@ -583,11 +684,11 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
       const int c = col(k0 + u);
-      if (c < N && (kbits[c >> 5] >> (c & 31) & 1u) && pb[u] < a.n) atomicOr(&words[pb[u] >> 5], 1u << (pb[u] & 31));
+      wave_set_bit(words, pb[u], c < N && (kbits[c >> 5] >> (c & 31) & 1u) && pb[u] < a.n);
     }
   }
   __syncthreads();
-  bitmap_prefix(words, a.nwords, blockpre, tmp);
+  bitmap_word_prefix(words, a.nwords, wpre, tmp);
   for (int k0 = 0; k0 < KPT; k0 += BATCH) {
     int32_t pb[BATCH];
     load_pos(k0, pb);
@@ -595,38 +696,11 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
     for (int u = 0; u < BATCH; ++u) {
       const int c = col(k0 + u);
       if (c >= N || !(kbits[c >> 5] >> (c & 31) & 1u) || pb[u] >= a.n) continue;
-      const int r = bitmap_rank(words, blockpre, pb[u]);
+      const int r = word_rank(words, wpre, pb[u]);
       if (r < k) {
         a.middle[int64_t(lg) * a.budget + r] = c;
         a.pos_new[int64_t(lg) * a.budget + P + r] = pb[u];
       }
-    }
-  }
-  if (lg != 0) return;
-  // Head (0, 0): protected columns ranked by position.
-  __syncthreads();
-  for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
-  __syncthreads();
-  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
-    int32_t pb[BATCH];
-    load_pos(k0, pb);
-#pragma unroll
-    for (int u = 0; u < BATCH; ++u) {
-      const int c = col(k0 + u);
-      if (c < N && is_protected(a, pb[u]) && pb[u] < a.n) atomicOr(&words[pb[u] >> 5], 1u << (pb[u] & 31));
-    }
-  }
-  __syncthreads();
-  bitmap_prefix(words, a.nwords, blockpre, tmp);
-  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
-    int32_t pb[BATCH];
-    load_pos(k0, pb);
-#pragma unroll
-    for (int u = 0; u < BATCH; ++u) {
-      const int c = col(k0 + u);
-      if (c >= N || !is_protected(a, pb[u]) || pb[u] >= a.n) continue;
-      const int r = bitmap_rank(words, blockpre, pb[u]);
-      if (r < P) a.prot_cols[r] = c;
     }
   }
 }
@@ -1467,9 +1541,9 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   a.pos_new = pos_new;
   a.nwords = int((n + 31) / 32);
   // The position bitmap (and its prefix counts) must fit in the LDS key array of the fast path.
-  const int64_t bitmap_words = a.nwords + (a.nwords + 31) / 32;
-  if (N <= SEL_LDS_KEYS && bitmap_words <= SEL_LDS_KEYS)
-    hipLaunchKernelGGL(select_row_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), 0, s, a);
+  // The position bitmap and its per-word prefix must fit in the LDS key array of the fast path.
+  if (N <= SEL_LDS_KEYS && 2 * int64_t(a.nwords) <= SEL_LDS_KEYS)
+    hipLaunchKernelGGL(select_row_kernel, dim3(unsigned(LG + 1)), dim3(SEL_THREADS), 0, s, a);
   else
     hipLaunchKernelGGL(select_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), select_lds_bytes(a.nwords), s, a);
   if (int rc = gse_launch_check("boundary select")) return rc;
