@@ -975,8 +975,8 @@ __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
   }
 }
 
-// Single-pass relocation for 8 KV heads x 64 dims, launched cooperatively (every workgroup
-// resident at once). Layer by layer, each wave loads its share of the moves (entries j0..j0+per
+// Single-pass relocation for 8 KV heads x 64 dims, launched with no more workgroups than the
+// device holds at once (every workgroup resident together). Layer by layer, each wave loads its share of the moves (entries j0..j0+per
 // of every head: lane (head lane/8, piece lane%8) carries 16 bytes of K and of V and, on piece 0,
 // the score) into registers, waits for the loads to land, and meets every other workgroup at a
 // grid barrier; then it writes them to their targets. All of a layer's sources are read before
@@ -1299,10 +1299,12 @@ BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t 
 }
 
 // Grid of the single-pass relocation: every workgroup the device can hold at once (cached per
-// device), and the moves per wave for a width of up to `budget`; no plan (0 blocks) when the
-// device lacks cooperative launch or a layer's moves do not fit in registers (8 per wave).
+// device), and the moves per wave for a width of up to `budget`; no plan (0 blocks) when a
+// layer's moves do not fit in registers (8 per wave), or GSE_RELOCATE_SCRATCH=1 (a deployment
+// that runs other kernels on concurrent streams, which could keep workgroups from being
+// resident together, selects the two-kernel path).
 void coop_plan(int64_t budget, int* blocks, int* per) {
-  static int cached[64] = {0};  // resident workgroups per device, -1 = no cooperative launch
+  static int cached[64] = {0};  // resident workgroups per device, -1 = unknown
   *blocks = *per = 0;
   // GSE_RELOCATE_SCRATCH=1 keeps the two-kernel path through scratch (tests run both).
   const char* force = getenv("GSE_RELOCATE_SCRATCH");
@@ -1310,9 +1312,8 @@ void coop_plan(int64_t budget, int* blocks, int* per) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
   if (!cached[dev]) {
-    int coop = 0, cus = 0, per_cu = 0;
-    const bool ok = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess && coop &&
-                    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+    int cus = 0, per_cu = 0;
+    const bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
                     hipOccupancyMaxActiveBlocksPerMultiprocessor(
                         &per_cu, reinterpret_cast<const void*>(&relocate_coop_kernel<8>), COOP_THREADS, 0) ==
                         hipSuccess &&
@@ -1555,11 +1556,14 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   int coop_blocks = 0, coop_per = 0;
   if (kv_heads == 8 && head_dim == 64) coop_plan(budget, &coop_blocks, &coop_per);
   if (coop_blocks > 0) {
-    void* args[] = {&b};
-    const void* fn = coop_per <= 4 ? reinterpret_cast<const void*>(&relocate_coop_kernel<4>)
-                                   : reinterpret_cast<const void*>(&relocate_coop_kernel<8>);
-    if (hipLaunchCooperativeKernel(fn, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), args, 0, s) != hipSuccess)
-      return gse_fail(GSE_ELAUNCH, "boundary: cooperative relocation launch failed");
+    // An ordinary launch of at most as many workgroups as the device holds at once: the stream's
+    // earlier kernels have retired before it starts, so every workgroup is resident.
+    // (hipLaunchCooperativeKernel guarantees the same but first drains the stream: each launch
+    // then left the GPU idle for about 0.5 ms.)
+    if (coop_per <= 4)
+      hipLaunchKernelGGL(relocate_coop_kernel<4>, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), 0, s, b);
+    else
+      hipLaunchKernelGGL(relocate_coop_kernel<8>, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), 0, s, b);
     if (int rc = gse_launch_check("boundary relocate")) return rc;
   } else if (kv_heads == 8 && head_dim == 64) {
     const dim3 rgrid(unsigned((budget + 4 * ROWS_PER_WAVE - 1) / (4 * ROWS_PER_WAVE)), unsigned(layers));
