@@ -197,7 +197,7 @@ class Workload:
             self.new_slots.append(nxt[:total_steps])
             st.entries[row] = e
             self.entries.append(e)
-            st.mode[row] = e["mode"]
+            st.mode[row] = ge.requests.score_word(e)
             st.count[row] = c
             st.frontier[row] = f
         st.req_to_token.copy_(r2t.to(dev))
@@ -465,7 +465,7 @@ def prefill_bench(args, torch, ge):
         st.scores.zero_()
         entry = ge._live_entry(SimpleNamespace(rid="prompt", session=None), cfg, "replay")
         st.entries[1] = entry
-        st.mode[1] = entry["mode"]
+        st.mode[1] = ge.requests.score_word(entry)
         resident = []
         for start in starts:
             count = min(chunk, prompt - start)

@@ -6,6 +6,13 @@
 // the budget goes to the highest float64 scores, exact ties keeping the newer
 // position. Positions are unique within a row, so the composite key
 // (ordered score bits, position) is unique and the top-k set is exact.
+//
+// New table row (R:466-468): the protected columns in position order, then the
+// kept middle (each head's survivors in position order at the shared targets).
+// Block policies (no reference counterpart) move the protected recent region
+// (from the first block of the recent window or sliding-window cursor to n)
+// after the middle, so a row's slot list always ends with its newest positions
+// in order.
 #include <algorithm>
 #include <cstdlib>
 
@@ -116,9 +123,13 @@ struct SelArgs {
   int64_t n_cols, n, budget, prefix, recent, cursor;
   int has_cursor, prefix_sliding, boundary_mode;
   int block;  // tokens per eviction block (1: token granularity)
+  // Protected positions at or past tail_from sit after the kept middle in the new table (n: none,
+  // the reference's layout; block policies: the recent region, see gse_boundary).
+  int64_t tail_from;
   uint64_t* keys;     // [LG, N]
   int32_t* posw;      // [LG, N]; protected stored as ~pos
   int32_t* prot_count;
+  int32_t* prot_low;  // [LG] protected positions below tail_from (boundary mode)
   uint8_t* kept_mask;  // public mode: [LG, N]
   // Boundary mode outputs.
   int32_t* middle;    // [LG, budget] kept middle columns sorted by position
@@ -191,7 +202,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
   int32_t* posw = a.posw + int64_t(lg) * N;
 
   // Phase 1: positions, protection and ordered score keys.
-  int nprot = 0;
+  int nprot = 0, nlow = 0;
   for (int64_t c = threadIdx.x; c < N; c += SEL_THREADS) {
     int64_t p;
     double sc = 0.0;
@@ -202,6 +213,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
     }
     const bool prot = is_protected(a, p);
     nprot += prot;
+    nlow += prot && p < a.tail_from;
     if (!prot && !a.prefix_sliding) {
       if (!a.boundary_mode) {
         sc = a.src.score[int64_t(lg) * N + c];
@@ -218,7 +230,11 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
     posw[c] = prot ? ~int32_t(p) : int32_t(p);
   }
   const int P = block_sum(nprot, tmp);
-  if (threadIdx.x == 0) a.prot_count[lg] = P;
+  const int Q = block_sum(nlow, tmp);  // the kept middle starts at column Q of the new table
+  if (threadIdx.x == 0) {
+    a.prot_count[lg] = P;
+    if (a.prot_low) a.prot_low[lg] = Q;
+  }
   const int64_t M = N - P;
   int64_t k = kept_width(a.budget, P, a.block, a.prefix_sliding);
   if (k < 0) k = 0;  // deferred: keep nothing beyond the protected set
@@ -309,7 +325,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
     const int r = bitmap_rank(words, blockpre, pw);
     if (r < k) {
       a.middle[int64_t(lg) * a.budget + r] = int32_t(c);
-      a.pos_new[int64_t(lg) * a.budget + P + r] = pw;
+      a.pos_new[int64_t(lg) * a.budget + Q + r] = pw;
     }
   }
   if (lg != 0) return;
@@ -511,8 +527,8 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
     }
   };
 
-  // Phase 1: hi keys, protection count, common high bits of the unprotected keys.
-  int nprot = 0;
+  // Phase 1: hi keys, protection counts, common high bits of the unprotected keys.
+  int nprot = 0, nlow = 0;
   uint32_t kand = 0xffffffffu, kor = 0u;
   for (int k0 = 0; k0 < KPT; k0 += BATCH) {
     int32_t pb[BATCH];
@@ -539,6 +555,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
           kor |= hi;
         }
         nprot += prot;
+        nlow += prot && pb[u] < a.tail_from;
         keys[c] = hi;
       }
     }
@@ -554,13 +571,17 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
     redu[1][wave] = kor;
   }
   const int P = block_sum(nprot, tmp);  // synchronises the workgroup
+  const int Q = block_sum(nlow, tmp);   // the kept middle starts at column Q of the new table
   kand = 0xffffffffu;
   kor = 0u;
   for (int w = 0; w < SEL_THREADS / 64; ++w) {
     kand &= redu[0][w];
     kor |= redu[1][w];
   }
-  if (threadIdx.x == 0) a.prot_count[lg] = P;
+  if (threadIdx.x == 0) {
+    a.prot_count[lg] = P;
+    a.prot_low[lg] = Q;
+  }
   const int M = N - P;
   int k = int(kept_width(a.budget, P, a.block, a.prefix_sliding));
   if (k < 0) k = 0;  // deferred: keep nothing beyond the protected set
@@ -699,7 +720,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
       const int r = word_rank(words, wpre, pb[u]);
       if (r < k) {
         a.middle[int64_t(lg) * a.budget + r] = c;
-        a.pos_new[int64_t(lg) * a.budget + P + r] = pb[u];
+        a.pos_new[int64_t(lg) * a.budget + Q + r] = pb[u];
       }
     }
   }
@@ -737,6 +758,7 @@ struct BndArgs {
   int64_t pstride;
   int32_t* slots;
   int32_t* prot_count;
+  int32_t* prot_low;  // [LG] protected positions below the tail region (head 0's sets the layout)
   int32_t* middle;
   int32_t* prot_cols;
   int32_t* targets;
@@ -766,7 +788,9 @@ __global__ void prep_slots_kernel(BndArgs a) {
 }
 
 // Single workgroup: validate the per-head protected counts, split the
-// unprotected columns into targets and leftover, write the new table row.
+// unprotected columns into targets and leftover, write the new table row:
+// protected columns below the tail region (Q of them, by position), the width
+// targets, then the remaining protected columns (Q = P for the reference's policies).
 __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   int* tmp = reinterpret_cast<int*>(lds);
@@ -819,6 +843,7 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
   if (bc[0] != GSE_BOUNDARY_EVICTED) return;
   const int P = bc[1];
   const int64_t width = bc[2];
+  const int Q = a.prot_low[0];
   for (int i = threadIdx.x; i < a.nwords_cols; i += SEL_THREADS) words[i] = 0;
   __syncthreads();
   for (int i = threadIdx.x; i < P; i += SEL_THREADS) {
@@ -828,7 +853,7 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
   __syncthreads();
   int32_t* trow = a.table + int64_t(a.row) * a.table_stride;
   // Unprotected columns in column order, 32 per thread per pass: target j = rank j < width
-  // (also the table's column P + j), leftover beyond.
+  // (also the table's column Q + j), leftover beyond.
   int carry = 0;
   for (int base = 0; base < a.nwords_cols; base += SEL_THREADS) {
     const int w = base + threadIdx.x;
@@ -858,7 +883,7 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
       if (!(bits >> t & 1u)) continue;
       if (j < width) {
         a.targets[j] = sl[t];
-        trow[P + j] = sl[t];
+        trow[Q + j] = sl[t];
       } else {
         a.leftover[j - width] = int64_t(sl[t]);
       }
@@ -866,7 +891,7 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
     }
     carry += total;
   }
-  for (int i = threadIdx.x; i < P; i += SEL_THREADS) trow[i] = a.slots[a.prot_cols[i]];
+  for (int i = threadIdx.x; i < P; i += SEL_THREADS) trow[i < Q ? i : width + i] = a.slots[a.prot_cols[i]];
   if (threadIdx.x == 0) {
     a.count[a.row] = int32_t(P + width);
     a.frontier[a.row] = int32_t(a.n);
@@ -1054,15 +1079,17 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
   }
 }
 
-// pos_new[l, g, i] = pos(l, g, prot_cols[i]) for the protected prefix of every head row.
+// pos_new[l, g, i'] = pos(l, g, prot_cols[i]) for the protected columns of every head row, at
+// the table's layout: i' = i below Q, width + i past it.
 __global__ __launch_bounds__(256) void protected_pos_kernel(BndArgs a) {
   const gse_boundary_status st = *a.status;
   if (st.state != GSE_BOUNDARY_EVICTED) return;
   const int lg = blockIdx.x;
+  const int Q = a.prot_low[0];
   for (int i = threadIdx.x; i < st.protected_count; i += blockDim.x) {
     const int64_t c = a.prot_cols[i];
     const int64_t p = c < a.row_count ? int64_t(a.pos_old[int64_t(lg) * a.pstride + c]) : a.row_frontier + c - a.row_count;
-    a.pos_new[int64_t(lg) * a.budget + i] = int32_t(p);
+    a.pos_new[int64_t(lg) * a.budget + (i < Q ? i : st.width + i)] = int32_t(p);
   }
 }
 
@@ -1288,7 +1315,7 @@ BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t 
   L.slots = o; o += align256(((N + 31) / 32) * 32 * 4);  // whole 32-column words
   L.keys = o; o += align256(LG * N * 8);
   L.posw = o; o += align256(LG * N * 4);
-  L.prot = o; o += align256(LG * 4);
+  L.prot = o; o += align256(2 * LG * 4);  // protected counts, then the counts below the tail region
   L.middle = o; o += align256(LG * budget * 4);
   L.prot_cols = o; o += align256(budget * 4);
   L.targets = o; o += align256(budget * 4);
@@ -1443,6 +1470,7 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   b.pstride = pos_old_stride;
   b.slots = reinterpret_cast<int32_t*>(ws + L.slots);
   b.prot_count = reinterpret_cast<int32_t*>(ws + L.prot);
+  b.prot_low = b.prot_count + LG;
   b.middle = reinterpret_cast<int32_t*>(ws + L.middle);
   b.prot_cols = reinterpret_cast<int32_t*>(ws + L.prot_cols);
   b.targets = reinterpret_cast<int32_t*>(ws + L.targets);
@@ -1534,9 +1562,18 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   a.prefix_sliding = b.prefix_sliding;
   a.boundary_mode = 1;
   a.block = block;
+  // Block policies place the protected recent region (the blocks of the recent window and of the
+  // sliding-window cursor, [tail_from, n)) after the kept middle, so every row's slot list ends
+  // with its newest positions in order: a score delay is then a cut of the list's last entries.
+  a.tail_from = n;
+  if (blk) {
+    const int64_t edge = std::max<int64_t>(0, std::min(n - recent, has_cursor ? cursor : n));
+    a.tail_from = edge - edge % block;
+  }
   a.keys = reinterpret_cast<uint64_t*>(ws + L.keys);
   a.posw = reinterpret_cast<int32_t*>(ws + L.posw);
   a.prot_count = b.prot_count;
+  a.prot_low = b.prot_low;
   a.middle = b.middle;
   a.prot_cols = b.prot_cols;
   a.pos_new = pos_new;

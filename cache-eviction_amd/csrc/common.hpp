@@ -13,6 +13,11 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 // Wavefront size on CDNA is 64.
 constexpr int kWave = 64;
 
+// A score word (a row's mode_by_row entry, a prefill call's mode): the score mode in bits 0-7
+// (1 sum, 2 max over a KV head's query heads) and the score delay above it, in list entries.
+GSE_DEVICE int score_kind(int32_t word) { return word & 0xff; }
+GSE_DEVICE int score_delay(int32_t word) { return word >> GSE_SCORE_DELAY_SHIFT; }
+
 GSE_DEVICE float bf16_to_f32(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
 
 // Round-to-nearest-even float -> bf16 (NaN stays NaN).

@@ -266,7 +266,7 @@ struct MergeArgs {
   uint16_t* o;
   int64_t o_sb, o_sh;
   float* norm_out;  // [bs, q_heads]
-  // Score queue (GSE_SCORE_QUEUE): for rows whose mode is 1 or 2, entry n = qcount[row] gets
+  // Score queue (GSE_SCORE_QUEUE): for rows whose score mode is 1 or 2, entry n = qcount[row] gets
   // the step's query, normaliser and list length if n < cap, and qcount[row] = n + 1 (a count
   // above cap records dropped steps).
   const uint16_t* q;
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(MERGE_THREADS * SPLIT) void decode_merge_kernel(Mer
   bool queue = false;
   if (a.qq) {
     row = load_index_dyn(a.rows, a.rows_dtype, b);
-    const int md = a.mode[row];
+    const int md = score_kind(a.mode[row]);
     slot = a.qcount[row] & QUEUE_COUNT_MASK;
     queue = md == 1 || md == 2;
   }
@@ -424,8 +424,9 @@ struct ScoreArgs {
 };
 
 // Grid (splits, bs), 512 threads: wave g = KV head g over keys [split*chunk, +chunk) of
-// sequence b. Per 16 keys, Sp = Q . K^T ([16 heads x 16 keys], heads 8-15 padding), so a
-// lane holds 4 heads of one key: sum / max over heads is in-lane plus one lane swap.
+// sequence b (the list's first len - delay entries). Per 16 keys, Sp = Q . K^T ([16 heads x
+// 16 keys], heads 8-15 padding), so a lane holds 4 heads of one key: sum / max over heads is
+// in-lane plus one lane swap.
 template <typename IdxT>
 __global__ __launch_bounds__(512) void decode_score_kernel(ScoreArgs a) {
   const int b = blockIdx.y;
@@ -435,11 +436,12 @@ __global__ __launch_bounds__(512) void decode_score_kernel(ScoreArgs a) {
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int64_t row = load_index_dyn(a.rows, a.rows_dtype, b);
-  const int md = a.mode[row];
+  const int word = a.mode[row];
+  const int md = score_kind(word);
   if (md != 1 && md != 2) return;
   const bool max_mode = md == 2;
   const int base = a.indptr[b];
-  const int len = a.indptr[b + 1] - base;
+  const int len = a.indptr[b + 1] - base - score_delay(word);  // keys the query scores
   const int k0 = blockIdx.x * a.chunk;
   const int k_end = k0 + a.chunk < len ? k0 + a.chunk : len;
   if (k0 >= k_end) return;

@@ -5,7 +5,7 @@
 // length to a per-(layer, row) queue. This pass adds the queued queries' H2O
 // scores to every key they saw, the reference's per-step update (R:189-200)
 // applied for a batch of steps at once:
-//   scores[l, g, slot(c)] += sum_i [c < lim_i] (sum | max)_{h in g} exp(q_ih . k_cg * scale - norm_ih)
+//   scores[l, g, slot(c)] += sum_i [c < lim_i - delay] (sum | max)_{h in g} exp(q_ih . k_cg * scale - norm_ih)
 // where slot(c) = table[row, c] for c < count[row], else req_to_token[row, frontier[row] + c - count[row]]
 // (the list of `fill`, R:136-152); every queued list is a prefix of the current one
 // because lists only grow between boundaries, and boundaries flush first.
@@ -147,15 +147,17 @@ __global__ __launch_bounds__(fl::THREADS) void score_flush_kernel(FlushArgs a) {
   const int lg = blockIdx.z;
   const int l = lg / a.kv_heads, g = lg % a.kv_heads;
   const int64_t row = load_index_dyn(a.rows, a.rows_dtype, blockIdx.y);
-  const int md = a.mode[row];
+  const int word = a.mode[row];
+  const int md = score_kind(word);
   if (md != 1 && md != 2) return;
   const int64_t qbase = int64_t(l) * a.rows_total + row;  // (layer, row) queue index
   int m = a.pcount[qbase];
   m = m < a.cap ? m : a.cap;
   if (m <= 0) return;
 
-  // Queued lengths: the workgroup's keys are [c0, min(c0 + CHUNK, max lim)).
-  if (threadIdx.x < m) lims[threadIdx.x] = a.plim[qbase * a.cap + threadIdx.x];
+  // Scored lengths (queued list length - the row's score delay): the workgroup's keys are
+  // [c0, min(c0 + CHUNK, max lim)).
+  if (threadIdx.x < m) lims[threadIdx.x] = max(0, a.plim[qbase * a.cap + threadIdx.x] - score_delay(word));
   __syncthreads();
   int maxlim = 0;
   for (int i = 0; i < m; ++i) maxlim = lims[i] > maxlim ? lims[i] : maxlim;

@@ -8,7 +8,8 @@
 //   S = Q . K^T   [16 rows x 16 keys] per row-block and key-block (16x16x32 bf16)
 // Pass 1 streams the visible keys once to get each row's log-sum-exp (with the
 // sink); pass 2 streams them again, turns logits into probabilities with that
-// normaliser and accumulates column sums.
+// normaliser and accumulates column sums (with a score delay d, only of the keys
+// at least d entries before each query: the causal bound of pass 2 moves back by d).
 //
 // Work per (query head, key) is one exp2 per pass, which bounds the kernel (v_exp_f32 runs
 // at half the rate of an FMA): pass 1 keeps a lazily rescaled running maximum per row (one
@@ -55,6 +56,7 @@ struct PrefillArgs {
   int q_heads, kv_heads;
   float scale2;
   float* norm2;  // [count, q_heads] row normalisers in log2 units (sink included)
+  int delay;     // pass 2 credits query i's keys k <= prefix_len + i - delay only
 };
 
 // One 64-key tile of a wave: row-block rb's MFMAs for four 16-key blocks, then per logit one
@@ -164,9 +166,11 @@ __global__ __launch_bounds__(64 * pf::waves<PASS>()) void prefill_kernel(Prefill
   const int64_t qb0 = (nqb - 1 - int64_t(blockIdx.x / a.kv_heads)) * QB;
   const int64_t i0 = qb0 + 2 * RB * wave;  // this wave's first query
   const int64_t last_q = (qb0 + QB < a.count ? qb0 + QB : a.count) - 1;
-  const int64_t kend = a.prefix_len + last_q + 1;  // keys any query of the workgroup sees
+  // Pass 2 credits keys up to `shift` entries before each query's causal bound.
+  const int64_t shift = PASS == 2 ? a.delay : 0;
+  const int64_t kend = a.prefix_len + last_q + 1 - shift;  // keys any query of the workgroup sees (scores)
   const bool wave_live = i0 < a.count;
-  const int64_t wave_kend = a.prefix_len + (i0 + 2 * RB - 1 < a.count ? i0 + 2 * RB - 1 : a.count - 1) + 1;
+  const int64_t wave_kend = a.prefix_len + (i0 + 2 * RB - 1 < a.count ? i0 + 2 * RB - 1 : a.count - 1) + 1 - shift;
 
   // A fragments: row col of row-block rb is query i0 + 2*rb + col/8, head g*8 + col%8;
   // lane supplies dims [16*grp, 16*grp + 16) as two 8-dim MFMA halves.
@@ -238,7 +242,7 @@ __global__ __launch_bounds__(64 * pf::waves<PASS>()) void prefill_kernel(Prefill
       }
       // Keys past the wave's first query need the causal mask (at most the last two tiles).
       float cs[4] = {0.f, 0.f, 0.f, 0.f};
-      const int64_t qpos0 = a.prefix_len + i0;
+      const int64_t qpos0 = a.prefix_len + i0 - shift;
       if (t0 + KT - 1 > qpos0)
         prefill_tile<PASS, MAX_MODE, true, RB>(qa, kb0, kb1, ref, sum, cs, a.scale2, t0 + col - qpos0, grp);
       else
@@ -515,7 +519,9 @@ extern "C" int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_s
                                   void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
   if (head_dim != pf::D || kv_heads < 1 || q_heads != pf::GROUP * kv_heads)
     return gse_fail(GSE_ESHAPE, "prefill: need head_dim 64 and q_heads == 8 * kv_heads");
-  if (mode != 1 && mode != 2) return gse_fail(GSE_EINVAL, "prefill: mode must be 1 (sum) or 2 (max)");
+  const int kind = mode & 0xff, delay = mode >> GSE_SCORE_DELAY_SHIFT;
+  if (kind != 1 && kind != 2) return gse_fail(GSE_EINVAL, "prefill: mode must be 1 (sum) or 2 (max)");
+  if (delay < 0) return gse_fail(GSE_EINVAL, "prefill: negative score delay");
   if (count < 0 || prefix_len < 0 || total != prefix_len + count)
     return gse_fail(GSE_EINVAL, "prefill: total must equal prefix_len + count");
   if (count == 0) return GSE_OK;
@@ -526,13 +532,13 @@ extern "C" int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_s
     return gse_fail(GSE_EWORKSPACE, "prefill: workspace too small");
   PrefillArgs a = {static_cast<const uint16_t*>(q), q_stride_t, q_stride_h, count,
                    static_cast<const uint16_t*>(k_pool), kv_stride_s, kv_stride_h, slots, slots_dtype, total,
-                   prefix_len, sinks, sinks_dtype, mode, scores, scores_stride_g, scores_stride_s, q_heads, kv_heads,
-                   sm_scale * kLog2e, static_cast<float*>(workspace)};
+                   prefix_len, sinks, sinks_dtype, kind, scores, scores_stride_g, scores_stride_s, q_heads, kv_heads,
+                   sm_scale * kLog2e, static_cast<float*>(workspace), delay};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t blocks = (count + pf::QB - 1) / pf::QB * kv_heads;
   if (blocks >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "prefill: chunk too large");
   const dim3 grid{static_cast<uint32_t>(blocks)};
-  if (mode == 2) {
+  if (kind == 2) {
     hipLaunchKernelGGL((prefill_kernel<1, true>), grid, dim3(64 * pf::waves<1>()), 0, s, a);
     if (int rc = gse_launch_check("prefill pass 1")) return rc;
     hipLaunchKernelGGL((prefill_kernel<2, true>), grid, dim3(64 * pf::waves<2>()), 0, s, a);

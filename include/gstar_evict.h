@@ -18,7 +18,10 @@
  *                           runtime keeps the KV heads of a slot adjacent (strides
  *                           slots*kv_heads, 1, kv_heads), so one page's scores fill whole lines
  *   table / req_to_token    int32 [rows, width]
- *   frontier / count / mode int32 [rows]
+ *   frontier / count / mode int32 [rows]; a mode word (mode_by_row[row], and the `mode`
+ *                           of gse_prefill_scores) holds the score mode in bits 0-7 (1 sum,
+ *                           2 max over a KV head's query heads, else no scores) and the
+ *                           score delay in bits 8-30 (GSE_SCORE_DELAY_SHIFT)
  *   pos (per row)           int32 [full layers, kv_heads, count]
  */
 #ifndef GSTAR_EVICT_H
@@ -56,6 +59,16 @@ enum {
   GSE_SCORE_QUEUE = 2  /* this step's query is queued; gse_score_flush adds the queued   */
                        /* queries' scores (one K pass per queue)                         */
 };
+
+/*
+ * Score delay (block policies; no reference counterpart, the reference report's ARC-AGI-3 runs
+ * count a block's attention only after 128 tokens, TEX:197): with delay d = word >> 8, a query
+ * at list length lim (its own key being entry lim - 1) adds scores to entries c < lim - d only.
+ * A block-policy boundary leaves the row's newest positions at the end of its table (the
+ * protected recent region after the kept middle), so with d <= recent these are exactly the
+ * keys at least d positions older than the query. d = 0 is the reference's update.
+ */
+#define GSE_SCORE_DELAY_SHIFT 8
 
 /* Boundary outcome written to device memory by gse_boundary. */
 enum {
@@ -115,7 +128,8 @@ int64_t gse_decode_workspace_bytes(int bs, int q_heads, int head_dim);
  *   o[b, h]       = sum_s softmax([q_h.k_s*scale, sink_h])_s v_s  (sink column dropped)
  *   norm_out[b,h] = log(exp(sink_h) + sum_s exp(q_h.k_s*scale))    (may be null)
  *   scores[g, slot_s] += sum_{h in g} p_hs  (mode 1)  or  max_{h in g} p_hs  (mode 2)
- * where mode = mode_by_row[rows[b]]; rows whose mode is not 1 or 2 get no score.
+ * where mode = mode_by_row[rows[b]] & 0xff, for the list's entries s < len - delay (the
+ * word's score delay); rows whose mode is not 1 or 2 get no score.
  * score_mode GSE_SCORE_EAGER adds the scores before returning (max_len bounds
  * every sequence's list length); GSE_SCORE_QUEUE appends the step to the row's
  * queue instead: queue_count[row] = n + 1 for n = queue_count[row], and if n < queue_cap
@@ -144,7 +158,7 @@ int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * layer, and empty their queues. No reference counterpart as an entry point: the
  * reference adds each step's scores eagerly (R:189-200, R:218-224); this applies
  * the same update for all queued steps at once:
- *   scores[l, g, slot(c)] += sum_i [c < lim_i] (sum | max)_{h in g} exp(q_ih . k_cg * scale - norm_ih)
+ *   scores[l, g, slot(c)] += sum_i [c < lim_i - delay] (sum | max)_{h in g} exp(q_ih . k_cg * scale - norm_ih)
  * with slot(c) = table[row, c] for c < count[row], else req_to_token[row, frontier[row] + c - count[row]]
  * (the list of `fill`). k_pools is a device array of `layers` pointers; the queue
  * buffers are those of gse_decode for layer 0, each layer's `rows_total` rows after
@@ -216,6 +230,9 @@ int64_t gse_boundary_workspace_bytes(int layers, int kv_heads, int head_dim, int
  *   targets/leftover = non-protected slots in column order split at width    (R:447-451)
  *   K, V, score of (middle[l,g,j], g) -> (targets[j], g) for every full layer (R:455-463)
  *   table[row] = slots[protected cols] ++ targets; count; frontier = n        (R:468-473)
+ *   (block policies: slots[protected cols before the recent region] ++ targets ++ slots[the
+ *   recent region's protected cols], the region starting at the first block of min(n - recent,
+ *   cursor); pos_new in the same column order)
  * k_pools / v_pools are device arrays of `layers` device pointers. pos_old rows
  * are pos_old_stride elements apart. Writes pos_new [L, G, budget] (first
  * `count` columns valid), leftover slots (int64, N - count of them) and
@@ -266,7 +283,9 @@ int gse_boundary_live(float* scores, int layers, int64_t scores_stride_l, int kv
  * prefill_scores — one extend chunk's exact per-KV-head column sums, added to
  * the score table (R:314-340, `_probabilities` + `_prefill_scores`):
  *   p[h, i, k] = exp(q_i,h . k_k * scale - logaddexp(logsumexp_k'(...), sink_h)),  k <= prefix_len + i
- *   scores[g, slots[k]] += sum_i (sum_{h in g} | max_{h in g}) p[h, i, k]
+ *   scores[g, slots[k]] += sum_i (sum_{h in g} | max_{h in g}) p[h, i, k] [k <= prefix_len + i - delay]
+ * with mode & 0xff (1 sum, 2 max) and the score delay of the mode word (the normaliser still
+ * covers every key k <= prefix_len + i).
  * q [count, q_heads, head_dim] bf16, keys gathered through slots (int64 or
  * int32, prefix slots then the chunk's own) from the pool. head_dim = 64,
  * q_heads = 8 * kv_heads. MFMA 16x16x32 bf16 tiles, two passes (row

@@ -84,7 +84,9 @@ def _decode_setup(lengths, seed=0, slots=20000):
     return b, st, q, sinks, perm, indptr, rows
 
 
-def _oracle_step(b, st, q, sinks, perm, indptr, lid, mode):
+def _oracle_step(b, st, q, sinks, perm, indptr, lid, mode, delay=0):
+    """Each sequence's attention and scores; its list holds positions 0..len-1 (no boundary yet),
+    so a score delay credits the keys at least `delay` positions before the query (len - 1)."""
     keys = b.token_to_kv_pool.get_key_buffer(lid).float().cpu().numpy()
     values = b.token_to_kv_pool.get_value_buffer(lid).float().cpu().numpy()
     qn = q.float().cpu().numpy()
@@ -98,17 +100,21 @@ def _oracle_step(b, st, q, sinks, perm, indptr, lid, mode):
         o, norm = O.decode_attention(qn[i], keys, values, slots, s, 0.125)
         outs.append(o)
         norms.append(norm)
-        O.decode_scores_into(scores, qn[i], keys, slots, norm, 0.125, mode)
+        O.decode_scores_into(scores, qn[i], keys, slots, norm, 0.125, mode, np.arange(len(slots)), len(slots) - 1,
+                             delay)
     return np.stack(outs), np.stack(norms), scores
 
 
 @pytest.mark.parametrize("mode", [1, 2])
 @pytest.mark.parametrize("queued", [False, True])
-def test_fused_decode_matches_oracle(mode, queued):
+@pytest.mark.parametrize("delay", [0, 100])
+def test_fused_decode_matches_oracle(mode, queued, delay):
+    """Attention and scores; a score delay of 100 (block policies) leaves the 37-key list unscored
+    and the others' newest 100 keys."""
     lengths = [37, 1500, 3001]
     b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths)
     st.score_mode = "queue" if queued else "eager"
-    st.mode[:] = mode
+    st.mode[:] = mode | delay << 8
     b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=perm)
     fb = SimpleNamespace(out_cache_loc=torch.zeros(3, dtype=torch.int64, device="cuda"), req_pool_indices=rows,
                          seq_lens_cpu=torch.tensor(lengths))
@@ -120,7 +126,7 @@ def test_fused_decode_matches_oracle(mode, queued):
         for i, r in enumerate(rows.tolist()):
             st.req_to_token[r, :lengths[i]] = perm[indptr[i]:indptr[i + 1]].int()
         ge.flush(st)
-    want_o, want_norm, want_scores = _oracle_step(b, st, q, sinks, perm, indptr, 1, mode)
+    want_o, want_norm, want_scores = _oracle_step(b, st, q, sinks, perm, indptr, 1, mode, delay)
     got_o = o.float().cpu().numpy()
     # bf16 output: P is rounded to bf16 before the PV product, as in SGLang's decode kernel.
     np.testing.assert_allclose(got_o, want_o, rtol=2e-2, atol=2e-2)
@@ -163,9 +169,10 @@ def test_queue_over_steps_equals_eager():
     torch.testing.assert_close(results[True], results[False], rtol=1e-5, atol=1e-8)
 
 
-@pytest.mark.parametrize("mode", [1, 2])
-def test_after_decode_rebuilds_normaliser_from_split_lse(mode):
-    """T:48-78 with SGLang's split LSE layout (splits [1, 5, 8]) produced by the oracle."""
+@pytest.mark.parametrize("mode,delay", [(1, 0), (2, 0), (1, 64)])
+def test_after_decode_rebuilds_normaliser_from_split_lse(mode, delay):
+    """T:48-78 with SGLang's split LSE layout (splits [1, 5, 8]) produced by the oracle; with a
+    score delay the newest `delay` keys of each list get nothing."""
     lengths = [37, 1500, 3001]
     b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths, seed=4)
     splits = [1, 5, 8]
@@ -178,7 +185,7 @@ def test_after_decode_rebuilds_normaliser_from_split_lse(mode):
     b.forward_metadata = SimpleNamespace(attn_lse=torch.tensor(lse, device="cuda"), kv_indptr=indptr,
                                          kv_indices=perm, num_kv_splits=torch.tensor(splits, dtype=torch.int32,
                                                                                       device="cuda"))
-    st.mode[:] = mode
+    st.mode[:] = mode | delay << 8
     ge.after_decode(b, q.reshape(3, -1), layer(1), SimpleNamespace(
         out_cache_loc=torch.zeros(3, dtype=torch.int64, device="cuda"), req_pool_indices=rows), sinks)
     expected = np.zeros(tuple(st.scores.shape[1:]))
@@ -186,7 +193,8 @@ def test_after_decode_rebuilds_normaliser_from_split_lse(mode):
         rows_keys = perm[indptr[i]:indptr[i + 1]].cpu().numpy()
         qn = q[i].float().cpu().numpy()
         _, norm = O.decode_attention(qn, keys, keys, rows_keys, sinks.float().cpu().numpy(), 0.125)
-        O.decode_scores_into(expected, qn, keys, rows_keys, norm, 0.125, mode)
+        O.decode_scores_into(expected, qn, keys, rows_keys, norm, 0.125, mode, np.arange(len(rows_keys)),
+                             len(rows_keys) - 1, delay)
     torch.testing.assert_close(st.scores[0].cpu(), torch.tensor(expected, dtype=torch.float32), rtol=2e-3, atol=1e-6)
     assert float(st.scores[1:].abs().sum()) == 0.0
 

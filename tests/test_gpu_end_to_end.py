@@ -9,6 +9,12 @@ does its host part, so the device state is checked in between and the entry afte
 scores, the boundary's retained positions, table, req_to_token, relocated K/V/scores and freed
 slots (bit-exact, the oracle ranking the GPU's own pre-boundary scores), each step's attention
 output, and the accumulated scores after the last step.
+
+The block policies (no reference counterpart) run the same flow with a score delay of 128
+positions, which the oracle applies by position (a query credits keys at least 128 positions
+older) and the kernels by cutting each list's last 128 entries: equal scores show that every
+list ends with its newest positions in order, before and after the boundary. One of them caps
+the evicted blocks so that the boundary keeps more than the budget (3072 of 2048).
 """
 import sys
 import types
@@ -68,7 +74,20 @@ def _assert_same_positions(got, want, scores, slot_of):
     raise AssertionError("retained positions differ in order only")
 
 
-def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang):
+CONFIGS = {
+    "head_sum": ({"name": "head_sum_2048"}, BUDGET),
+    # 16-token layer-shared blocks, delay 128, at most 64 blocks evicted: the boundary at 4096 keeps
+    # 4096 - 64 * 16 = 3072 columns.
+    "block_sum_capped": ({"name": "block_sum_2048", "block": 16, "shared": True, "score_delay": 128,
+                          "max_evicted_blocks": 64}, 3072),
+    # The reference report's settings: 4-token blocks scored by their maximum, delay 128, cap 512.
+    "block_max_report": ({"name": "block_max_2048", "block": 4, "shared": True, "score_delay": 128,
+                          "max_evicted_blocks": 512}, BUDGET),
+}
+
+
+@pytest.mark.parametrize("case", list(CONFIGS))
+def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang, case):
     ge = fake_sglang
     g = torch.Generator().manual_seed(0)
     slots_total = PROMPT + STEPS + 64
@@ -82,7 +101,9 @@ def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang):
     slot_of = (torch.randperm(slots_total - 1, generator=g)[:PROMPT + STEPS] + 1).cuda()
     keys, values = b.token_to_kv_pool.get_key_buffer(0), b.token_to_kv_pool.get_value_buffer(0)
 
-    cfg = {"name": "head_sum_2048", "budget": BUDGET, "prefix": PREFIX, "recent": RECENT, "seed": 0}
+    extra, kept = CONFIGS[case]
+    cfg = {"budget": BUDGET, "prefix": PREFIX, "recent": RECENT, "seed": 0, **extra}
+    delay = cfg.get("score_delay", 0)
     lengths = [0]
     req = _request(cfg, lengths)
     batch = SimpleNamespace(reqs=[req], tree_cache=SimpleNamespace(token_to_kv_pool_allocator=alloc))
@@ -90,6 +111,7 @@ def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang):
     ost = O.OracleState([keys.float().cpu().numpy()], [values.float().cpu().numpy()],
                         st.req_to_token.cpu().numpy())
     oe = O.live_entry(cfg)
+    mode = oe["mode"]
     kn, sn = ost.keys[0], sinks.float().cpu().numpy()
     rows = torch.tensor([ROW], device="cuda")
 
@@ -114,9 +136,9 @@ def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang):
         # Oracle chunk scores, 256 queries at a time (the probability tile stays small).
         pre = slot_of[:start].cpu().numpy()
         for lo in range(0, CHUNK, 256):
-            upd, sl = O.prefill_score_update(1, q_all[start + lo:start + lo + 256].float().cpu().numpy(), kn, sn,
-                                             SCALE, 8, np.concatenate((pre, new[:lo].cpu().numpy())),
-                                             new[lo:lo + 256].cpu().numpy())
+            upd, sl = O.prefill_score_update(mode, q_all[start + lo:start + lo + 256].float().cpu().numpy(), kn,
+                                             sn, SCALE, 8, np.concatenate((pre, new[:lo].cpu().numpy())),
+                                             new[lo:lo + 256].cpu().numpy(), delay=delay)
             ost.scores[0][:, sl] += upd.astype(np.float32)
     entry = st.entries[ROW]
     assert [ev["after"] for ev in entry["events"]] == [CHUNK] == [ev["after"] for ev in oe["events"]]
@@ -138,19 +160,20 @@ def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang):
             ofreed = []
             O.boundary(ost, ROW, oe, p, p - 128, free=ofreed.append)
             assert len(st.pending) == 1 and entry["count"] == 0 and not freed
-            assert np.array_equal(st.table[ROW, :BUDGET].cpu().numpy(), ost.table[ROW, :BUDGET])
+            assert oe["count"] == kept
+            assert np.array_equal(st.table[ROW, :kept].cpu().numpy(), ost.table[ROW, :kept])
             assert np.array_equal(st.req_to_token[ROW].cpu().numpy(), ost.req_to_token[ROW])
-            assert int(st.count[ROW]) == BUDGET and int(st.frontier[ROW]) == p
+            assert int(st.count[ROW]) == kept and int(st.frontier[ROW]) == p
             assert np.array_equal(keys.float().cpu().numpy(), ost.keys[0])
             assert np.array_equal(values.float().cpu().numpy(), ost.values[0])
             assert np.array_equal(st.scores.cpu().numpy(), ost.scores)
         if t == 1:
             # The next decode hook finished it.
             assert not st.pending
-            assert entry["count"] == oe["count"] == BUDGET and entry["frontier"] == PROMPT
+            assert entry["count"] == oe["count"] == kept and entry["frontier"] == PROMPT
             _assert_same_positions(entry["pos"].cpu().numpy(), oe["pos"], pre_scores, slot_of.cpu().numpy())
             assert np.array_equal(torch.cat(freed).cpu().numpy(), ofreed[0])
-            assert [ev["after"] for ev in entry["events"]][-1] == BUDGET
+            assert [ev["after"] for ev in entry["events"]][-1] == kept
         # SGLang's allocation of the new token, then the CSR and the fused decode.
         new = slot_of[p:p + 1]
         st.req_to_token[ROW, p] = new.int()
@@ -167,7 +190,11 @@ def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang):
         qn = q_all[p].float().cpu().numpy()
         want_o, norm = O.decode_attention(qn, ost.keys[0], ost.values[0], res, sn, SCALE)
         ost.scores[:, :, int(new)] = 0.0
-        O.decode_scores_into(ost.scores[0], qn, ost.keys[0], res, norm, SCALE, 1)
+        key_pos = np.arange(p + 1)
+        if oe["count"]:
+            tail = np.arange(oe["frontier"], p + 1)
+            key_pos = np.concatenate((oe["pos"][0], np.broadcast_to(tail, (8, tail.size))), axis=1)
+        O.decode_scores_into(ost.scores[0], qn, ost.keys[0], res, norm, SCALE, mode, key_pos, p, delay)
         want_outs.append(want_o)
     ge.flush(st)
     got = torch.stack(outs).float().cpu().numpy()

@@ -35,17 +35,20 @@ def _case(count, prefix_len, seed, slots=20000):
     return b, st, q, sinks, perm[:prefix_len].cuda(), perm[prefix_len:].cuda()
 
 
-@pytest.mark.parametrize("count,prefix_len,mode", [(1, 0, 1), (37, 0, 2), (100, 300, 1), (257, 1000, 2),
-                                                   (130, 64, 1)])
-def test_prefill_scores_match_oracle(count, prefix_len, mode):
+@pytest.mark.parametrize("count,prefix_len,mode,delay", [
+    (1, 0, 1, 0), (37, 0, 2, 0), (100, 300, 1, 0), (257, 1000, 2, 0), (130, 64, 1, 0),
+    # Score delays (block policies): pass 2 credits keys `delay` positions older than each query
+    # only, while pass 1's normaliser covers the whole causal range.
+    (257, 1000, 2, 128), (130, 64, 1, 100), (37, 0, 1, 5), (200, 0, 2, 190), (20, 30, 1, 60)])
+def test_prefill_scores_match_oracle(count, prefix_len, mode, delay):
     b, st, q, sinks, prefix, new = _case(count, prefix_len, seed=count + prefix_len)
     keys = b.token_to_kv_pool.get_key_buffer(1)
     before = torch.rand(st.scores.shape, generator=torch.Generator().manual_seed(3)).cuda()
     st.scores.copy_(before)
-    ge._prefill_scores(st, 0, mode, layer(1), q, keys, sinks, prefix, new)
+    ge._prefill_scores(st, 0, mode | delay << 8, layer(1), q, keys, sinks, prefix, new)
     upd, slots = O.prefill_score_update(mode, q.float().cpu().numpy(), keys.float().cpu().numpy(),
                                         sinks.float().cpu().numpy(), 0.125, 8, prefix.cpu().numpy(),
-                                        new.cpu().numpy())
+                                        new.cpu().numpy(), delay=delay)
     expected = before.clone()
     expected[0][:, torch.tensor(slots).cuda()] += torch.tensor(upd, dtype=torch.float32).cuda()
     torch.testing.assert_close(st.scores, expected, rtol=1e-3, atol=1e-6)
