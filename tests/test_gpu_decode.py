@@ -297,13 +297,16 @@ def test_merge_of_empty_short_and_long_sequences_over_a_reused_workspace():
         ge.STATE = None
 
 
-@pytest.mark.parametrize("bs", [40, 3])
+@pytest.mark.parametrize("bs", [40, 3, 300])
 def test_merge_paths_for_many_and_few_sequences(bs):
     """The merge folds a sequence's partials in one group when there are at least 32 sequences
     (about 8 workgroups each) and in 8 groups combined through LDS below that (one sequence spread
-    over up to 256 workgroups): both against the oracle, outputs and queued normalisers."""
+    over up to 256 workgroups): both against the oracle, outputs and queued normalisers. With
+    more sequences than workgroups (300 lists of 0-59 keys), a workgroup's range holds several
+    whole sequences, empty ones included."""
     g = np.random.default_rng(bs)
-    lengths = [int(x) for x in g.integers(1, 400 if bs > 8 else 6000, size=bs)]
+    lo, hi = (0, 60) if bs > 256 else (1, 400 if bs > 8 else 6000)
+    lengths = [int(x) for x in g.integers(lo, hi, size=bs)]
     b, st, q, sinks, perm, indptr, rows = _decode_setup(lengths, seed=30 + bs, slots=40000)
     st.score_mode = "queue"
     st.mode[:] = 1
@@ -319,6 +322,10 @@ def test_merge_paths_for_many_and_few_sequences(bs):
     index = st.index[1]
     norms = st.qnorm[index, 1:bs + 1, 0].cpu().numpy()
     for i in range(bs):
+        if lengths[i] == 0:  # all mass on the sink
+            assert np.all(got[i] == 0.0)
+            np.testing.assert_allclose(norms[i], sn, rtol=1e-6, atol=1e-6)
+            continue
         want_o, want_norm = O.decode_attention(q[i].float().cpu().numpy(), keys, values, pm[ip[i]:ip[i + 1]], sn, 0.125)
         np.testing.assert_allclose(got[i], want_o, rtol=2e-2, atol=2e-2)
         np.testing.assert_allclose(norms[i], want_norm, rtol=1e-5, atol=1e-4)
