@@ -1,0 +1,117 @@
+"""The scheduler hooks' refusals, on CPU tensors (no kernel runs): invalid configs, retracted
+requests, chunks that rewind below the frontier or cross a 2048 boundary, and rows that change
+hands. Each turns the request inert with the reference's error text and policy mode 0
+(R:625-637, R:640-689); a retraction also writes its payload (R:668-674)."""
+import sys
+import types
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from fakes import backend
+
+
+@pytest.fixture
+def hooks(monkeypatch, tmp_path):
+    monkeypatch.setenv("GSTAR_PAYLOAD_DIR", str(tmp_path))
+    names = ["sglang", "sglang.srt", "sglang.srt.mem_cache", "sglang.srt.mem_cache.unified_cache",
+             "sglang.srt.mem_cache.unified_cache.component_type"]
+    for name in names:
+        monkeypatch.setitem(sys.modules, name, types.ModuleType(name))
+    sys.modules[names[-1]].ComponentType = SimpleNamespace(SWA="swa")
+    import gstar_evict
+    gstar_evict.STATE = None
+    gstar_evict.RETRACTED.clear()
+    st = gstar_evict.state(backend(rows=4, width=8192, slots=64, layers=2, full=(0,), device="cpu"))
+    yield gstar_evict, st, tmp_path
+    gstar_evict.STATE = None
+    gstar_evict.RETRACTED.clear()
+
+
+CFG = {"name": "head_sum_2048", "budget": 2048, "prefix": 128, "recent": 512, "seed": 0}
+
+
+def _req(rid, row, start, length, params=None, retraction=0):
+    return SimpleNamespace(rid=rid, session=None, retraction_count=retraction,
+                           sampling_params=SimpleNamespace(custom_params=params),
+                           extend_range=SimpleNamespace(start=start, length=length),
+                           kv=SimpleNamespace(req_pool_idx=row, get_evicted_seqlen=lambda kind: 0))
+
+
+def _extend(ge, *reqs):
+    ge.on_extend(SimpleNamespace(reqs=list(reqs), tree_cache=SimpleNamespace(token_to_kv_pool_allocator=None)))
+
+
+def test_valid_config_gets_a_mode_and_a_fresh_row(hooks):
+    ge, st, _ = hooks
+    st.frontier[1], st.count[1] = 77, 5  # stale state from a previous owner of the row
+    _extend(ge, _req("a", 1, 0, 2048, {"gstar_eviction": CFG}))
+    e = st.entries[1]
+    assert e["error"] is None and e["kind"] == "live" and int(st.mode[1]) == 1
+    assert int(st.frontier[1]) == 0 and int(st.count[1]) == 0
+
+
+@pytest.mark.parametrize("cfg,message", [
+    ({**CFG, "prefix": 2000}, "invalid gstar eviction settings"),          # P + R > B
+    ({**CFG, "name": "lru_2048"}, "invalid gstar eviction settings"),       # unknown policy
+    ({**CFG, "name": "prefix_sliding_2048"}, "Prefix Sliding requires B = P + R"),
+    ({k: v for k, v in CFG.items() if k != "budget"}, "'budget'"),          # missing key
+])
+def test_invalid_config_runs_unevicted(hooks, cfg, message):
+    ge, st, _ = hooks
+    _extend(ge, _req("a", 1, 0, 2048, {"gstar_eviction": cfg}))
+    e = st.entries[1]
+    assert message in e["error"] and e["mode"] == 0 and int(st.mode[1]) == 0
+
+
+def test_requests_without_params_get_no_entry(hooks):
+    ge, st, _ = hooks
+    _extend(ge, _req("a", 1, 0, 2048, None), _req("b", 2, 0, 2048, {"other": 1}))
+    assert st.entries == {}
+
+
+def test_retracted_request_is_refused_and_stays_refused(hooks):
+    ge, st, tmp = hooks
+    from gstar_evict import retention
+    _extend(ge, _req("a", 1, 0, 2048, {"gstar_eviction": CFG}, retraction=1))
+    e = st.entries[1]
+    assert e["error"] == "retracted" and int(st.mode[1]) == 0 and "a" in ge.RETRACTED
+    doc = retention.read_payload(tmp / "a-retracted.json.gz")
+    assert doc["kind"] == "retracted" and doc["cfg"] == CFG
+    # The same request on a fresh row (its key is remembered) is refused too.
+    _extend(ge, _req("a", 2, 0, 2048, {"gstar_eviction": CFG}))
+    assert st.entries[2]["error"] == "retracted" and int(st.mode[2]) == 0
+
+
+def test_rewind_below_the_frontier_is_an_error(hooks):
+    ge, st, _ = hooks
+    _extend(ge, _req("a", 1, 0, 2048, {"gstar_eviction": CFG}))
+    st.entries[1]["frontier"] = 4096  # as after a boundary at 4096
+    _extend(ge, _req("a", 1, 2048, 1024, {"gstar_eviction": CFG}))
+    assert st.entries[1]["error"] == "the session rewound below the eviction frontier"
+    assert int(st.mode[1]) == 0
+
+
+@pytest.mark.parametrize("start,length,ok", [(2000, 48, True), (2000, 49, False), (100, 1948, True),
+                                             (4000, 200, False), (2049, 2047, True), (2049, 2048, False)])
+def test_chunk_crossing_a_boundary_is_an_error(hooks, start, length, ok):
+    ge, st, _ = hooks
+    _extend(ge, _req("a", 1, start, length, {"gstar_eviction": CFG}))
+    e = st.entries[1]
+    if ok:
+        assert e["error"] is None and int(st.mode[1]) == 1
+    else:
+        assert e["error"] == "prefill chunk crosses a boundary; use --chunked-prefill-size 2048"
+        assert int(st.mode[1]) == 0
+
+
+def test_errors_keep_the_row_inert_and_a_new_owner_starts_clean(hooks):
+    ge, st, _ = hooks
+    _extend(ge, _req("a", 1, 2000, 100, {"gstar_eviction": CFG}))
+    assert st.entries[1]["error"]
+    _extend(ge, _req("a", 1, 2100, 100, {"gstar_eviction": CFG}))  # later chunks: still refused
+    assert st.entries[1]["error"] and int(st.mode[1]) == 0
+    _extend(ge, _req("b", 1, 0, 2048, {"gstar_replay": CFG}))  # the row changes hands
+    e = st.entries[1]
+    assert e["key"] == "b" and e["kind"] == "replay" and e["error"] is None and int(st.mode[1]) == 1
