@@ -719,7 +719,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
       if (c >= N || !(kbits[c >> 5] >> (c & 31) & 1u) || pb[u] >= a.n) continue;
       const int r = word_rank(words, wpre, pb[u]);
       if (r < k) {
-        a.middle[int64_t(lg) * a.budget + r] = c;
+        a.middle[int64_t(lg) * a.budget + r] = int32_t(c);
         a.pos_new[int64_t(lg) * a.budget + Q + r] = pb[u];
       }
     }
@@ -738,6 +738,7 @@ constexpr int COOP_WAVES = COOP_THREADS / 64;
 constexpr int COOP_GROUPS = 8;
 constexpr int COOP_SLEEP = 20;
 constexpr int COOP_SPIN_LIMIT = 1 << 18;
+constexpr int COOP_MAX_LAYERS = 128;  // pool pointer tables held in LDS
 
 
 struct BndArgs {
@@ -759,7 +760,7 @@ struct BndArgs {
   int32_t* slots;
   int32_t* prot_count;
   int32_t* prot_low;  // [LG] protected positions below the tail region (head 0's sets the layout)
-  int32_t* middle;
+  int32_t* middle;  // [LG, budget] each head's j-th kept middle column (its slot: slots[column])
   int32_t* prot_cols;
   int32_t* targets;
   int32_t* pos_new;
@@ -912,8 +913,7 @@ __global__ __launch_bounds__(256) void relocate_kernel(BndArgs a) {
   const int64_t j = t / chunks;
   const int piece = int(t % chunks);
   if (j >= width) return;
-  const int32_t col = a.middle[int64_t(lg) * a.budget + j];
-  const int64_t src = a.slots[col], dst = a.targets[j];
+  const int64_t src = a.slots[a.middle[int64_t(lg) * a.budget + j]], dst = a.targets[j];
   auto K = as_global(static_cast<uint16_t*>(a.k_pools[l]));
   auto V = as_global(static_cast<uint16_t*>(a.v_pools[l]));
   const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
@@ -1001,80 +1001,146 @@ __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
 }
 
 // Single-pass relocation for 8 KV heads x 64 dims, launched with no more workgroups than the
-// device holds at once (every workgroup resident together). Layer by layer, each wave loads its share of the moves (entries j0..j0+per
-// of every head: lane (head lane/8, piece lane%8) carries 16 bytes of K and of V and, on piece 0,
-// the score) into registers, waits for the loads to land, and meets every other workgroup at a
-// grid barrier; then it writes them to their targets. All of a layer's sources are read before
-// any of its targets is written, as the two-kernel path through scratch guarantees (R:455-464),
-// at half its HBM traffic. A layer's stores and the next layer's loads touch different pools, so
-// one barrier per layer suffices. The barrier's wait is bounded: past 2^18 polls (about 0.3 s) a workgroup
-// stops waiting and marks the boundary GSE_BOUNDARY_ERR_RELOCATE, which the host raises.
+// device holds at once (every workgroup resident together). It runs in phases, two per layer:
+// the layer's K pool with its scores, then its V pool. In a phase each wave loads its share of
+// the moves (entries j0..j0+per of every head: lane (head lane/8, piece lane%8) carries 16 bytes
+// and, for K, the head's score) into registers; once they have landed its workgroup arrives at
+// the phase's grid barrier, issues the next phase's loads, waits for every other workgroup and
+// then writes the phase's rows to their targets. All of a pool's sources are read before any of
+// its targets is written, as the two-kernel path through scratch guarantees (R:455-464), at half
+// its HBM traffic, and the next pool's loads are in flight while the barrier completes (each
+// pool is written in exactly one phase, so loads of a later phase never meet a store of an
+// earlier one). A barrier's wait is bounded: past 2^18 polls (about 0.3 s) a workgroup stops
+// waiting, marks the boundary GSE_BOUNDARY_ERR_RELOCATE, which the host raises, and waits no more.
 
-GSE_DEVICE void grid_barrier(BndArgs& a, uint32_t layer) {
-  // Every load of this workgroup has returned before it arrives.
+// The wave's loaded registers are in use here: the compiler waits for exactly these loads.
+GSE_DEVICE void landed(const uint4& x) { asm volatile("" ::"v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w)); }
+GSE_DEVICE void landed(float x) { asm volatile("" ::"v"(x)); }
+
+// Arrival at phase `phase`'s barrier, after every wave of the workgroup has its loads. Counters
+// 64 words (256 bytes) apart: the top one, then group k's (workgroups k, k + 8, ...); a group's
+// last arrival bumps the top one, so no address takes more than 32 atomics per barrier.
+GSE_DEVICE void grid_arrive(BndArgs& a, uint32_t phase) {
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
   if (threadIdx.x == 0) {
-    // Counters 64 words (256 bytes) apart: the top one, then group k's (workgroups k, k + 8, ...).
-    uint32_t* top = a.grid_arrivals;
     const uint32_t grp = blockIdx.x % COOP_GROUPS;
     const uint32_t members = (gridDim.x - grp + COOP_GROUPS - 1) / COOP_GROUPS;
     uint32_t* cnt = a.grid_arrivals + 64 * (1 + grp);
     const uint32_t before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (before + 1 == (layer + 1) * members) __hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before + 1 == (phase + 1) * members)
+      __hip_atomic_fetch_add(a.grid_arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Wait until every workgroup has arrived at phase `phase` (thread 0 polls, sleeping 20 x 64
+// cycles between reads); `gave_up` (thread 0's) ends all waiting after a timeout.
+GSE_DEVICE void grid_wait(BndArgs& a, uint32_t phase, bool& gave_up) {
+  if (threadIdx.x == 0 && !gave_up) {
     const uint32_t groups = gridDim.x < uint32_t(COOP_GROUPS) ? gridDim.x : uint32_t(COOP_GROUPS);
-    const uint32_t target = (layer + 1) * groups;
+    const uint32_t target = (phase + 1) * groups;
     int spins = 0;
-    while (__hip_atomic_load(top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+    while (__hip_atomic_load(a.grid_arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
       __builtin_amdgcn_s_sleep(COOP_SLEEP);
       if (++spins > COOP_SPIN_LIMIT) {
         atomicExch(&a.status->state, int32_t(GSE_BOUNDARY_ERR_RELOCATE));
+        gave_up = true;
         break;
       }
     }
   }
-  __syncthreads();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 template <int PER>
 __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) {
+  // The pool pointers in LDS: their reads wait on the LDS counter, not on the vector memory
+  // counter that the phase's loads and stores hold.
+  __shared__ uint16_t* pools[2][COOP_MAX_LAYERS];
   const gse_boundary_status st = *a.status;
   if (st.state != GSE_BOUNDARY_EVICTED || st.width <= 0) return;  // the same for every workgroup
+  for (int i = threadIdx.x; i < a.layers; i += COOP_THREADS) {
+    pools[0][i] = static_cast<uint16_t*>(a.k_pools[i]);
+    pools[1][i] = static_cast<uint16_t*>(a.v_pools[i]);
+  }
+  __syncthreads();
   const int64_t width = st.width;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 3, piece = lane & 7;
   const int64_t nwaves = int64_t(gridDim.x) * COOP_WAVES;
   const int64_t per = (width + nwaves - 1) / nwaves;  // <= PER (checked by the host for the budget)
-  const int64_t j0 = (int64_t(blockIdx.x) * COOP_WAVES + (threadIdx.x >> 6)) * per;
-  for (int l = 0; l < a.layers; ++l) {
-    const int lg = l * a.kv_heads + g;
-    auto K = as_global(static_cast<uint16_t*>(a.k_pools[l]));
-    auto V = as_global(static_cast<uint16_t*>(a.v_pools[l]));
-    const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
-    float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
-    uint4 kv[PER][2];
-    float sc[PER];
-    int64_t dst[PER];
+  // Entries, and so their targets, are the same for the whole wave (scalar registers).
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int64_t j0 = (int64_t(blockIdx.x) * COOP_WAVES + wave) * per;
+  const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
+  // Entry r of the wave is j0 + r if r < per and j0 + r < width; the others repeat entry
+  // width - 1, whose wave moves the same bytes to the same target in the same phase. Every load
+  // and store is unconditional (a head's 8 lanes all write its score), so the compiler counts
+  // them exactly and each wait covers only the loads it needs.
+  int32_t jc[PER], dst[PER];
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    jc[r] = int32_t(r < per && j0 + r < width ? j0 + r : width - 1);
+    dst[r] = a.targets[jc[r]];
+  }
+  int32_t src[PER];
+  uint4 kd[PER], vd[PER];
+  float sc[PER];
+  auto sources = [&](int l) {
+    const int32_t* m = a.middle + int64_t(l * a.kv_heads + g) * a.budget;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) src[r] = a.slots[m[jc[r]]];
+  };
+  auto load_k = [&](int l) {
+    auto K = as_global(static_cast<const uint16_t*>(pools[0][l]));
+    const float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
-      const int64_t j = j0 + r;
-      dst[r] = -1;
-      if (r < per && j < width) {
-        const int64_t src = a.slots[a.middle[int64_t(lg) * a.budget + j]];
-        dst[r] = a.targets[j];
-        kv[r][0] = gload16(K + src * a.kv_ss + off);
-        kv[r][1] = gload16(V + src * a.kv_ss + off);
-        sc[r] = srow[src * a.sss];
+      kd[r] = gload16(K + int64_t(src[r]) * a.kv_ss + off);
+      sc[r] = srow[int64_t(src[r]) * a.sss];
+    }
+  };
+  auto load_v = [&](int l) {
+    auto V = as_global(static_cast<const uint16_t*>(pools[1][l]));
+#pragma unroll
+    for (int r = 0; r < PER; ++r) vd[r] = gload16(V + int64_t(src[r]) * a.kv_ss + off);
+  };
+  bool gave_up = false;
+  sources(0);
+  load_k(0);
+  for (int l = 0; l < a.layers; ++l) {
+    // Phase 2l: layer l's K rows and scores.
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      landed(kd[r]);
+      landed(sc[r]);
+    }
+    grid_arrive(a, uint32_t(2 * l));
+    load_v(l);
+    if (l + 1 < a.layers) sources(l + 1);  // the V loads have taken their addresses
+    grid_wait(a, uint32_t(2 * l), gave_up);
+    {
+      auto K = as_global(pools[0][l]);
+      float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
+#pragma unroll
+      for (int r = 0; r < PER; ++r) {
+        gstore16(K + int64_t(dst[r]) * a.kv_ss + off, kd[r]);
+        srow[int64_t(dst[r]) * a.sss] = sc[r];
       }
     }
-    grid_barrier(a, uint32_t(l));
+    // Phase 2l + 1: layer l's V rows.
 #pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      if (dst[r] < 0) continue;
-      gstore16(K + dst[r] * a.kv_ss + off, kv[r][0]);
-      gstore16(V + dst[r] * a.kv_ss + off, kv[r][1]);
-      if (piece == 0) srow[dst[r] * a.sss] = sc[r];
+    for (int r = 0; r < PER; ++r) landed(vd[r]);
+    grid_arrive(a, uint32_t(2 * l + 1));
+    if (l + 1 < a.layers) load_k(l + 1);
+    grid_wait(a, uint32_t(2 * l + 1), gave_up);
+    {
+      auto V = as_global(pools[1][l]);
+#pragma unroll
+      for (int r = 0; r < PER; ++r) gstore16(V + int64_t(dst[r]) * a.kv_ss + off, vd[r]);
     }
   }
 }
@@ -1591,7 +1657,7 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
   if (int rc = gse_launch_check("boundary columns")) return rc;
 
   int coop_blocks = 0, coop_per = 0;
-  if (kv_heads == 8 && head_dim == 64) coop_plan(budget, &coop_blocks, &coop_per);
+  if (kv_heads == 8 && head_dim == 64 && layers <= COOP_MAX_LAYERS) coop_plan(budget, &coop_blocks, &coop_per);
   if (coop_blocks > 0) {
     // An ordinary launch of at most as many workgroups as the device holds at once: the stream's
     // earlier kernels have retired before it starts, so every workgroup is resident.
