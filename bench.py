@@ -56,7 +56,12 @@ def parse(argv=None):
     p.add_argument("--decode-latency", action="store_true",
                    help="bs=1 decode layer latency at 8K/16K/32K resident (the reference's published shape)")
     p.add_argument("--prefill-policy", default="block_sum_2048",
-                   help="eviction policy of the --prefill workload (block policies: 16-token layer-shared blocks)")
+                   help="eviction policy of the --prefill workload (block policies: layer-shared blocks)")
+    p.add_argument("--prefill-block", type=int, default=16, help="positions per block of a --prefill block policy")
+    p.add_argument("--prefill-delay", type=int, default=0,
+                   help="score delay of a --prefill block policy (the reference report's ARC-AGI-3 runs: 128)")
+    p.add_argument("--prefill-cap", type=int, default=0,
+                   help="evicted blocks per boundary of a --prefill block policy, 0 = no cap (the report: 512)")
     p.add_argument("--prefill", action="store_true",
                    help="time the chunked-prefill score tiles instead: 12 layers, 79,720-token prompt in "
                         "8192-token chunks, prefix capped at the 28,672-token budget (MFMA roofline)")
@@ -451,9 +456,10 @@ def prefill_bench(args, torch, ge):
     layer_objs = [SimpleNamespace(sliding_window_size=-1, tp_q_head_num=HQ, tp_k_head_num=HKV, qk_head_dim=D,
                                   layer_id=l, scaling=D ** -0.5) for l in range(L)]
     cfg = {"name": args.prefill_policy, "budget": cap, "prefix": 512, "recent": 4096, "seed": args.seed}
-    if args.prefill_policy in ("block_sum_2048", "block_max_2048"):
-        cfg.update(block=16, shared=True)
-    mode = 2 if args.prefill_policy in ("head_max_sum_2048", "block_max_2048") else 1
+    block_policy = args.prefill_policy in ("block_sum_2048", "block_max_2048")
+    if block_policy:
+        cfg.update(block=args.prefill_block, shared=True, score_delay=args.prefill_delay,
+                   max_evicted_blocks=args.prefill_cap)
     starts = list(range(0, prompt, chunk))
     timing = {"score": [], "boundary": []}
 
@@ -464,8 +470,11 @@ def prefill_bench(args, torch, ge):
         st.frontier.zero_()
         st.scores.zero_()
         entry = ge._live_entry(SimpleNamespace(rid="prompt", session=None), cfg, "replay")
+        if entry["error"]:
+            raise ValueError(f"--prefill config: {entry['error']}")
         st.entries[1] = entry
-        st.mode[1] = ge.requests.score_word(entry)
+        word = ge.requests.score_word(entry)  # score mode and delay
+        st.mode[1] = word
         resident = []
         for start in starts:
             count = min(chunk, prompt - start)
@@ -477,7 +486,7 @@ def prefill_bench(args, torch, ge):
             prefix = torch.cat((st.table[1, :entry["count"]], st.req_to_token[1, entry["frontier"]:start]))
             new = st.req_to_token[1, start:start + count]
             for l in range(L):
-                ge._prefill_scores(st, l, mode, layer_objs[l], q[:count], keys[l], sinks, prefix, new)
+                ge._prefill_scores(st, l, word, layer_objs[l], q[:count], keys[l], sinks, prefix, new)
             ev[2].record()
             resident.append(prefix.numel())
             if record:
@@ -506,13 +515,17 @@ def prefill_bench(args, torch, ge):
     # and its score read and written (the width is the budget minus the 4608 protected).
     moved = sum(L * HKV * (ev["after"] - 4608) * (2 * 2 * D * 2 + 4 * 2) for ev in evictions)
     policy = args.prefill_policy.replace("_2048", "")
+    if block_policy:
+        policy += f" {args.prefill_block}-token layer-shared blocks"
+        policy += f", score delay {args.prefill_delay}" if args.prefill_delay else ""
+        policy += f", at most {args.prefill_cap} blocks evicted per boundary" if args.prefill_cap else ""
     return {
         "metric": "chunked-prefill score tiles, TFLOP/s (one QK^T pass) and % of bf16 MFMA peak",
         "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 1,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"gpt-oss-20b chunked prefill, {L} layers, 79,720-token prompt in 8192-token chunks, "
-                               f"{policy}{' 16-token layer-shared blocks' if 'block' in policy else ''}, budget {cap} "
+                               f"{policy}, budget {cap} "
                                f"(512+4096+24064), 5% heavy-hitter keys",
                    "causal_pairs_per_layer": pairs},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
