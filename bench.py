@@ -300,7 +300,9 @@ class Workload:
 
 def kernel_roofline(w, reps):
     """Average duration of the fused decode launch (split + merge kernels) over the last step's
-    inputs, with HIP events on the launch stream, and its algorithmic bytes per launch."""
+    inputs, with HIP events on the launch stream, and its algorithmic bytes per launch. One event
+    pair brackets each pass over the layers (12 launches back to back, as in a step), so the
+    average holds the launches and the gaps between them, not an event's own latency."""
     torch, ge, a = w.torch, w.ge, w.args
     bs = a.bs
     fb = SimpleNamespace(out_cache_loc=w.new_slots[max(w.step_index - 1, 0)], req_pool_indices=w.rows,
@@ -309,18 +311,16 @@ def kernel_roofline(w, reps):
     res = [w.resident(i) for i in range(bs)]
     per_launch = sum(attention_bytes(r) for r in res)
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps * a.layers)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps * a.layers)]
-    k = 0
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     torch.cuda.synchronize()
-    for _ in range(reps):
+    for k in range(reps):
+        starts[k].record(stream)
         for l in range(a.layers):
-            starts[k].record(stream)
             ge.decode(w.backend, w.q[l].view(bs, -1), w.layer_objs[l], fb, w.sinks[l], w.o[l].view(bs, -1))
-            ends[k].record(stream)
-            k += 1
+        ends[k].record(stream)
     torch.cuda.synchronize()
-    ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    ms = [s.elapsed_time(e) / a.layers for s, e in zip(starts, ends)]
     avg_us = 1000 * statistics.mean(ms)
     return per_launch, avg_us
 
