@@ -72,3 +72,10 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     rc = lib.gse_diagnose_chunk(None, 0, 0, 10, None, 0, 0, None, 0, 10, 0, None, 0, None, None, 0, 0, None, 2, 0,
                                 0, None, 0, 1.0, 64, 8, 64, 0.125, None, 0, None)
     assert rc != 0 and b"null pointer" in lib.gse_last_error()
+
+
+def test_score_word_layout_matches_the_header():
+    """The host packs a row's score delay above GSE_SCORE_DELAY_SHIFT, as the kernels unpack it."""
+    from gstar_evict import requests
+    m = re.search(r"#define\s+GSE_SCORE_DELAY_SHIFT\s+(\d+)", open(HEADER).read())
+    assert m and int(m.group(1)) == requests.SCORE_DELAY_SHIFT
