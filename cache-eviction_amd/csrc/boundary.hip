@@ -1076,14 +1076,16 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t j0 = (int64_t(blockIdx.x) * COOP_WAVES + wave) * per;
   const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
-  // Entry r of the wave is j0 + r if r < per and j0 + r < width; the others repeat entry
-  // width - 1, whose wave moves the same bytes to the same target in the same phase. Every load
-  // and store is unconditional (a head's 8 lanes all write its score), so the compiler counts
-  // them exactly and each wait covers only the loads it needs.
+  // Entry r of the wave is j0 + r up to its last one, min(j0 + per, width) - 1; the spare
+  // registers repeat that last entry (a wave with none repeats entries spread over the width),
+  // and a repeat moves the same bytes to the same target in the same phase as the entry's own
+  // move. Every load and store is unconditional (a head's 8 lanes all write its score), so the
+  // compiler counts them exactly and each wait covers only the loads it needs.
+  const int64_t last = (j0 + per < width ? j0 + per : width) - 1;
   int32_t jc[PER], dst[PER];
 #pragma unroll
   for (int r = 0; r < PER; ++r) {
-    jc[r] = int32_t(r < per && j0 + r < width ? j0 + r : width - 1);
+    jc[r] = int32_t(j0 + r <= last ? j0 + r : (j0 < width ? last : (j0 + r) % width));
     dst[r] = a.targets[jc[r]];
   }
   int32_t src[PER];
