@@ -1,4 +1,4 @@
-"""The north-star workload's own shape, checked through properties that do not depend on size:
+"""The bs=32 decode workload at full size, checked through properties that do not depend on size:
 12 full-attention layers of gpt-oss-20b shape, 32 sequences of 16K-64K tokens (random 16-token
 pages), a 32,768-position budget (512 + 4096 + 28,160), head_sum, a boundary every 64 decode
 steps (bench.py's default workload, built by its own Workload class).
@@ -18,7 +18,7 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-def test_boundary_at_the_north_star_shape():
+def test_boundary_at_the_bs32_32k_budget_decode_shape():
     if not torch.cuda.is_available():
         pytest.skip("needs a GPU")
     import bench
