@@ -99,6 +99,53 @@ def boundary_bytes(n_cols, width, count, freed, layers):
     return select + move + 4 * count + 8 * freed
 
 
+def precompacted_row(n, interval, budget, prefix, recent, slots, width, middle):
+    """A row of logical length n as its last boundary (at f = n - n % interval) left it, when
+    f > budget: the table holds the prefix, the recent window (protected, by position) and a
+    per-head sorted middle (``middle(lo, hi, count)`` draws [L, G, count] ascending positions in
+    [lo, hi)); req_to_token holds the owned prefix and middle slots packed at its start, the real
+    slots of the recent window [f - recent, f) and the tail [f, n) (the repack of R:485-491 with
+    the cursor past the recent window). ``slots`` are the row's slots in column order: table
+    columns first, then the tail. Rows with f <= budget hold positions 0..n-1 unevicted.
+    Returns CPU int32 tensors: table [count], req_to_token [width], pos [L, G, count]."""
+    import torch
+    f = n - n % interval
+    r2t = torch.zeros(width, dtype=torch.int32)
+    if f <= budget:
+        r2t[:n] = slots[:n].int()
+        return {"frontier": 0, "count": 0, "table": None, "req_to_token": r2t, "pos": None}
+    lo, hi, mid = prefix, f - recent, budget - prefix - recent
+    drawn = middle(lo, hi, mid).to(torch.int32)
+    layers, heads = drawn.shape[:2]
+    pos = torch.empty((layers, heads, budget), dtype=torch.int32)
+    pos[:, :, :prefix] = torch.arange(prefix, dtype=torch.int32)
+    pos[:, :, prefix:prefix + recent] = torch.arange(hi, f, dtype=torch.int32)
+    pos[:, :, prefix + recent:] = drawn
+    r2t[hi:f] = slots[prefix:prefix + recent].int()
+    packed = torch.cat((slots[:prefix], slots[prefix + recent:budget]))
+    r2t[:packed.numel()] = packed.int()
+    r2t[f:n] = slots[budget:budget + n - f].int()
+    return {"frontier": f, "count": budget, "table": slots[:budget].int(), "req_to_token": r2t, "pos": pos}
+
+
+def local_row_state(table_row, r2t_row, pos, count, frontier, n):
+    """A row's eviction state over a local slot numbering that holds only the row's own slots:
+    ``used`` (ascending global slot ids of the table and of req_to_token[:n]) maps global slot
+    used[j] to local slot j + 1; local slot 0 stays the null slot. The local table and
+    req_to_token are the global ones renumbered, so a boundary on them takes the same decisions
+    (ownership and sliding-window checks included) as on the live row. CPU int64 tensors."""
+    import torch
+    table = table_row[:count].long()
+    r2t = r2t_row[:n].long()
+    used = torch.unique(torch.cat((table, r2t[r2t > 0])))
+    local_r2t = torch.zeros(n, dtype=torch.int64)
+    held = r2t > 0
+    local_r2t[held] = torch.searchsorted(used, r2t[held]) + 1
+    local_table = torch.searchsorted(used, table) + 1
+    return {"used": used, "table": local_table, "req_to_token": local_r2t,
+            "pos": None if pos is None else pos.long(), "count": count, "frontier": frontier, "n": n}
+
+
 class Workload:
     """The synthetic serving state: pools, rows, eviction state, pre-drawn steps."""
 
@@ -169,36 +216,25 @@ class Workload:
         self.entries = []
         self.new_slots = []
         cfg = {"name": args.policy, "budget": B, "prefix": args.prefix, "recent": args.recent, "seed": args.seed}
+        def middle(lo, hi, mid):
+            draw = torch.rand((L * HKV, hi - lo), device=dev, generator=self.dgen)
+            return (draw.argsort(-1)[:, :mid].sort(-1).values + lo).view(L, HKV, mid).cpu()
+
         for i, r in enumerate(rows):
             row = i + 1
             s = self.row_slots[i]
             e = ge._live_entry(SimpleNamespace(rid=f"r{row}", session=None), cfg, "live")
-            n, f, c = r["len"], r["frontier"], r["count"]
+            n = r["len"]
+            init = precompacted_row(n, args.interval, B, args.prefix, args.recent, s, r2t.shape[1], middle)
+            f, c = init["frontier"], init["count"]
+            r2t[row] = init["req_to_token"]
             if c:
-                # Columns: prefix, recent window (protected, by position), then a per-head sorted middle.
-                lo, hi = args.prefix, f - args.recent
-                mid = B - args.prefix - args.recent
-                pos = torch.empty((L, HKV, B), dtype=torch.int32)
-                pos[:, :, :args.prefix] = torch.arange(args.prefix, dtype=torch.int32)
-                pos[:, :, args.prefix:args.prefix + args.recent] = torch.arange(hi, f, dtype=torch.int32)
-                draw = torch.rand((L * HKV, hi - lo), device=dev, generator=self.dgen)
-                ranks = draw.argsort(-1)[:, :mid].sort(-1).values + lo
-                pos[:, :, args.prefix + args.recent:] = ranks.view(L, HKV, mid).to(torch.int32).cpu()
-                table[row, :c] = s[:c].int()
-                # req_to_token after the last repack: real slots from `true` on, packed owned slots first.
-                true = f - args.recent
-                r2t[row, true:f] = s[args.prefix:args.prefix + args.recent].int()
-                packed = torch.cat((s[:args.prefix], s[args.prefix + args.recent:c]))
-                r2t[row, :packed.numel()] = packed.int()
-                tail = s[c:c + n - f]
-                r2t[row, f:n] = tail.int()
-                e["pos"] = pos.to(dev)
+                table[row, :c] = init["table"]
+                e["pos"] = init["pos"].to(dev)
                 e.update(frontier=f, count=c, last_boundary=f)
-                nxt = s[c + n - f:]
             else:
-                r2t[row, :n] = s[:n].int()
-                nxt = s[n:]
                 e["last_boundary"] = n - n % args.interval
+            nxt = s[c + n - f:]
             self.new_slots.append(nxt[:total_steps])
             st.entries[row] = e
             self.entries.append(e)
@@ -325,64 +361,107 @@ def kernel_roofline(w, reps):
     return per_launch, avg_us
 
 
-def cpu_baseline(w):
-    """Time the numpy oracle on a bounded sample of the same workload (2 sequences x 2 layers
-    decode at their real resident sets, one row boundary on 2 layers) and scale to the full
-    step (bs sequences x 12 layers, plus the measured boundary rate)."""
-    import numpy as np
-    import oracle as O
-    torch, a = w.torch, w.args
-    st = w.st
-    seqs, layers = 2, 2
-    t_dec = 0.0
-    for i in range(seqs):
-        row = i + 1
-        e = w.entries[i]
-        n = w.lens[i]
-        slots = torch.cat((st.table[row, :e["count"]], st.req_to_token[row, e["frontier"]:n])).long()
-        for l in range(layers):
-            keys = w.backend.token_to_kv_pool.get_key_buffer(l)[slots].float().cpu().numpy()
-            vals = w.backend.token_to_kv_pool.get_value_buffer(l)[slots].float().cpu().numpy()
-            q = w.q[l][i].float().cpu().numpy()
-            s = w.sinks[l].float().cpu().numpy()
-            local = np.arange(slots.numel())
-            t0 = time.perf_counter()
-            o, norm = O.decode_attention(q, keys, vals, local, s, D ** -0.5)
-            sc = np.zeros((HKV, slots.numel()))
-            O.decode_scores_into(sc, q, keys, local, norm, D ** -0.5, 1)
-            t_dec += time.perf_counter() - t0
-    per_seq_layer = t_dec / (seqs * layers)
-    # Boundary sample: the largest row's candidates on 2 layers, selection + relocation + repack
-    # (O.boundary) on a local pool holding just the row's candidate slots (local slot j + 1).
-    i = max(range(a.bs), key=lambda j: w.resident(j))
-    e = w.entries[i]
-    row, c, f, n = i + 1, e["count"], e["frontier"], w.lens[i]
-    N = c + n - f
-    slots = torch.cat((st.table[row, :c], st.req_to_token[row, f:n])).long()
-    pad = np.zeros((1, HKV, D), np.float32)
-    keys = [np.concatenate((pad, w.backend.token_to_kv_pool.get_key_buffer(l)[slots].float().cpu().numpy()))
-            for l in range(layers)]
-    vals = [np.concatenate((pad, w.backend.token_to_kv_pool.get_value_buffer(l)[slots].float().cpu().numpy()))
-            for l in range(layers)]
-    r2t = np.zeros((1, n + 1), np.int64)
-    r2t[0, f:n] = np.arange(c + 1, N + 1)
-    ost = O.OracleState(keys, vals, r2t, np.random.default_rng(0).random((layers, HKV, N + 1)).astype(np.float32))
-    ost.table[0, :c] = np.arange(1, c + 1)
-    oe = O.live_entry({"name": a.policy, "budget": a.budget, "prefix": a.prefix, "recent": a.recent,
-                       "seed": a.seed})
-    oe.update(frontier=f, count=c)
-    if c:
-        oe["pos"] = e["pos"][:layers].cpu().numpy().astype(np.int64)
-    t0 = time.perf_counter()
-    O.boundary(ost, 0, oe, n, None, free=lambda leftover: None)
-    t_sel = (time.perf_counter() - t0) * a.layers / layers
-    rate = w.boundaries / max(a.steps, 1)
-    us_step = 1e6 * (per_seq_layer * a.bs * a.layers + rate * t_sel)
-    return {"value": us_step, "unit": "us/step", "cores": 1, "kind": "port",
-            "sample": f"numpy float64 oracle: decode attention + head_sum scores for {seqs} sequences x {layers} "
-                      f"layers at their resident sets ({per_seq_layer * 1e3:.0f} ms each) scaled to {a.bs} x "
-                      f"{a.layers}; one {N}-candidate boundary (selection, K/V/score relocation, repack) on "
-                      f"{layers} layers scaled to {a.layers} layers at {rate:.2f} boundaries/step"}
+def cpu_threads():
+    """Host threads for the CPU baseline: the cores this process may run on, capped by
+    OMP_NUM_THREADS when the environment sets it (a host's share of its cores)."""
+    cores = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return min(cores, int(cap)) if cap.isdigit() and int(cap) > 0 else cores
+
+
+def median_time(fn, prepare=None, repeats=5):
+    """Median wall time of ``fn()`` over ``repeats`` runs after one warm-up run; ``prepare()``
+    (untimed) runs before each."""
+    times = []
+    for k in range(repeats + 1):
+        arg = prepare() if prepare is not None else None
+        t0 = time.perf_counter()
+        fn(arg)
+        if k:
+            times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_baseline(w, seqs=8, layers=2, repeats=5):
+    """The same step on the host cores: the torch-CPU restatement (oracle/torch_cpu.py) of
+    decode attention + H2O scores and of one row's boundary, on a bounded sample of this
+    workload's own state, one warm-up and the median of ``repeats`` runs each, scaled to a step.
+
+    Decode: ``seqs`` sequences spread over the resident-count range, ``layers`` layers each, at
+    their real CSR lists over a local pool of the sequence's slots; scaled by resident keys to
+    the batch and by layers to all full layers. Boundary: the evicting row with the most arriving
+    positions, its real table / req_to_token / retained positions renumbered onto a local pool
+    (``local_row_state``), on ``layers`` layers, scaled to all layers and to the measured
+    boundaries per step."""
+    import torch
+    from oracle import torch_cpu as TC
+    a, st, ge = w.args, w.st, w.ge
+    torch_threads = torch.get_num_threads()
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    try:
+        pool = w.backend.token_to_kv_pool
+
+        def local_state(i):
+            e, row, n = w.entries[i], i + 1, w.lens[i]
+            return local_row_state(st.table[row].cpu(), st.req_to_token[row].cpu(),
+                                   e["pos"][:layers].cpu() if e["count"] else None, e["count"], e["frontier"], n)
+
+        def local_pools(ls):
+            dev_used = ls["used"].to(st.device)
+            pad = torch.zeros((1, HKV, D), dtype=torch.bfloat16)
+            kp = [torch.cat((pad, pool.get_key_buffer(l)[dev_used].cpu())) for l in range(layers)]
+            vp = [torch.cat((pad, pool.get_value_buffer(l)[dev_used].cpu())) for l in range(layers)]
+            sc = torch.cat((torch.zeros((layers, HKV, 1)), st.scores[:layers][:, :, dev_used].cpu()), -1)
+            return kp, vp, sc
+
+        order = sorted(range(a.bs), key=w.resident)
+        sample = sorted({order[round(k * (a.bs - 1) / max(seqs - 1, 1))] for k in range(seqs)})
+        t_dec, keys_dec = 0.0, 0
+        for i in sample:
+            ls = local_state(i)
+            kp, vp, sc = local_pools(ls)
+            csr = torch.cat((ls["table"], ls["req_to_token"][ls["frontier"]:]))
+            for l in range(layers):
+                q, sinks = w.q[l][i].float().cpu(), w.sinks[l].float().cpu()
+                t_dec += median_time(lambda _: TC.decode_layer(q, kp[l], vp[l], csr, sinks, D ** -0.5, sc[l]),
+                                     repeats=repeats)
+                keys_dec += csr.numel()
+        total_keys = sum(w.resident(i) for i in range(a.bs)) * a.layers
+        us_decode = 1e6 * t_dec / keys_dec * total_keys
+
+        rows = [i for i in range(a.bs) if w.entries[i]["count"] and w.lens[i] > w.entries[i]["frontier"]]
+        i = max(rows, key=lambda j: w.lens[j] - w.entries[j]["frontier"]) if rows else None
+        us_boundary, candidates = 0.0, 0
+        if i is not None:
+            ls = local_state(i)
+            kp, vp, sc = local_pools(ls)
+            n = ls["n"]
+            candidates = ls["count"] + n - ls["frontier"]
+
+            def prepare():
+                return ([k.clone() for k in kp], [v.clone() for v in vp], sc.clone(), ls["table"].clone(),
+                        ls["req_to_token"].clone())
+
+            def run(state):
+                k, v, s, table, r2t = state
+                out = TC.boundary(k, v, s, table, r2t, ls["pos"], ls["count"], ls["frontier"], n, a.budget,
+                                  a.prefix, a.recent, n - 256, a.policy)
+                if out is None:
+                    raise RuntimeError("the sampled row did not evict")
+
+            t_b = median_time(run, prepare, repeats)
+            rate = w.boundaries / max(a.steps, 1)
+            us_boundary = 1e6 * t_b * a.layers / layers * rate
+    finally:
+        torch.set_num_threads(torch_threads)
+    return {"value": round(us_decode + us_boundary, 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "sample": f"torch-CPU fp32 restatement, {threads} threads, median of {repeats} after 1 warm-up: decode "
+                      f"attention + head_sum scores of {len(sample)} sequences x {layers} layers ({keys_dec} keys) "
+                      f"scaled by resident keys to {a.bs} sequences x {a.layers} layers "
+                      f"({round(us_decode)} us); one {candidates}-candidate row boundary (selection, K/V/score "
+                      f"relocation, repack) on {layers} layers scaled to {a.layers} layers x "
+                      f"{w.boundaries / max(a.steps, 1):.2f} boundaries/step ({round(us_boundary)} us)"}
 
 
 def measured_traffic():
@@ -795,7 +874,14 @@ def main():
         "evict_overhead_vs_attention": round((1000 * ms_step - args.layers * avg_us) / (args.layers * avg_us), 4),
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(w)
+        # The GPU measurement is complete here: a failure of the host-side baseline is reported in
+        # its field, never allowed to lose the line.
+        try:
+            result["cpu_baseline"] = cpu_baseline(w)
+        except Exception as problem:  # noqa: BLE001
+            import traceback
+            traceback.print_exc()
+            result["cpu_baseline"] = {"value": None, "unit": "us/step", "error": repr(problem)}
     print(json.dumps(result), flush=True)
 
 

@@ -1,0 +1,108 @@
+"""PyTorch-CPU restatement of the eviction path's per-step work: the CPU baseline.
+
+TEST INFRASTRUCTURE ONLY. ``bench.py``'s CPU-baseline leg times these functions on the host
+cores beside the GPU numbers, and ``tests/test_cpu_baseline.py`` checks them against the numpy
+oracle (``evict_oracle``); the product never imports this module.
+
+The reference path is torch code (R = code/cache_eviction/sglang_evict_runtime.py): decode
+attention with sinks plus the per-step score update (R:155-224, output closed form R:266-271),
+and the boundary (selection R:376-412, relocation and repack R:415-491). These functions restate
+the same arithmetic with torch's CPU kernels, vectorised over heads, fp32 for attention and
+scores (K/V stored as bf16 and upcast after the gather, as on the GPU), float64 for ranking.
+"""
+from __future__ import annotations
+
+import torch
+
+
+def decode_layer(q, k_pool, v_pool, slots, sinks, scale, scores, mode=1):
+    """One sequence's decode step on one full layer.
+
+    q [Hq, D] fp32; k_pool / v_pool [S, G, D] bf16 (the layer's pool); slots [N] int64 (the
+    sequence's CSR list); sinks [Hq] fp32; scores [G, S] fp32, updated in place with
+    ``sum_{h in g} p_hs`` (mode 1) or the max (mode 2) per resident slot (R:189-200).
+    Returns o [Hq, D] fp32 = softmax([q.k * scale, sink]) . v with the sink column dropped.
+    """
+    k = k_pool.index_select(0, slots).float()  # [N, G, D]
+    v = v_pool.index_select(0, slots).float()
+    heads, dim = q.shape
+    groups = k.shape[1]
+    qg = q.view(groups, heads // groups, dim)
+    logits = torch.bmm(qg, k.permute(1, 2, 0).contiguous()) * scale  # [G, g, N]
+    norm = torch.logaddexp(torch.logsumexp(logits, -1), sinks.view(groups, -1))
+    p = torch.exp(logits - norm[..., None])
+    o = torch.bmm(p, v.transpose(0, 1).contiguous())  # [G, g, D]
+    if mode in (1, 2):
+        scores.index_add_(1, slots, p.sum(1) if mode == 1 else p.amax(1))
+    return o.reshape(heads, dim)
+
+
+def boundary(k_pools, v_pools, scores, table_row, r2t_row, pos_old, count, frontier, n, budget, prefix,
+             recent, cursor=None, policy="head_sum_2048"):
+    """One row's live eviction boundary at logical length n (R:415-491), in place.
+
+    k_pools / v_pools: per full layer [S, G, D] (any dtype); scores [L, G, S] fp32; table_row /
+    r2t_row [W] int64 (the row's table and req_to_token); pos_old [L, G, count] int64 (the
+    retained positions; None when count is 0). Head policies rank the table scores, others
+    rank zeros (the timed baseline is the head policies').
+    Returns (new_count, pos_new [L, G, new_count], leftover slots), or None if the row is within
+    its budget or the boundary is deferred. Raises RuntimeError as R:389 and R:489 do.
+    """
+    cols = torch.cat((table_row[:count], r2t_row[frontier:n]))
+    size = cols.numel()
+    if size <= budget:
+        return None
+    layers, heads = scores.shape[:2]
+    pos = torch.empty((layers, heads, size), dtype=torch.int64)
+    pos[..., count:] = torch.arange(frontier, n)
+    if count:
+        pos[..., :count] = pos_old
+    first_tail = n - recent if cursor is None else min(n - recent, cursor)
+    prot = (pos < prefix) | (pos >= first_tail)
+    per_head = prot.sum(-1)
+    n_prot = int(per_head[0, 0])
+    if bool((per_head != n_prot).any()):
+        raise RuntimeError("protected positions differ between heads")
+    if n_prot > budget:
+        return None
+    if policy in ("head_sum_2048", "head_max_sum_2048"):
+        rank = scores[:, :, cols].double()
+    else:
+        rank = torch.zeros((layers, heads, size), dtype=torch.float64)
+    rank[prot] = float("inf")
+    # Order by (rank desc, position desc): positions are distinct within a row, so sorting by
+    # position first and then stably by rank gives the lexicographic order.
+    by_pos = torch.argsort(pos, dim=-1, descending=True)
+    by_rank = torch.argsort(rank.gather(-1, by_pos), dim=-1, descending=True, stable=True)
+    keep = by_pos.gather(-1, by_rank)[..., :budget]
+    prot_cols = keep[0, 0, :n_prot]
+    prot_cols = prot_cols[torch.argsort(pos[0, 0, prot_cols])]
+    is_prot = torch.zeros(size, dtype=torch.bool)
+    is_prot[prot_cols] = True
+    unprotected = torch.nonzero(~is_prot).flatten()  # column order
+    width = budget - n_prot
+    targets, leftover = cols[unprotected[:width]], cols[unprotected[width:]]
+    middle = keep[..., n_prot:]
+    middle_pos, order = pos.gather(-1, middle).sort(-1)
+    middle = middle.gather(-1, order)
+    source = cols[middle]  # [L, G, width] slots
+    head_ids = torch.arange(heads)
+    for l in range(layers):
+        src = source[l].t()  # [width, G]
+        # Advanced indexing reads every source row before the assignment writes a target.
+        moved_k, moved_v = k_pools[l][src, head_ids], v_pools[l][src, head_ids]
+        moved_s = scores[l][head_ids[:, None], source[l]]
+        k_pools[l][targets[:, None], head_ids] = moved_k
+        v_pools[l][targets[:, None], head_ids] = moved_v
+        scores[l][:, targets] = moved_s
+    table = torch.cat((cols[prot_cols], targets))
+    new_pos = torch.cat((pos[..., prot_cols], middle_pos), -1)
+    table_row[:table.numel()] = table
+    scores[:, :, leftover] = 0.0
+    true_len = min(n - recent, n if cursor is None else cursor)
+    own = table[~torch.isin(table, r2t_row[true_len:n])]
+    if own.numel() > true_len:
+        raise RuntimeError("packed ownership overlaps the sliding-window region")
+    r2t_row[:true_len] = 0
+    r2t_row[:own.numel()] = own
+    return table.numel(), new_pos, leftover

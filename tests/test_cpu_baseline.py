@@ -1,0 +1,119 @@
+"""The CPU baseline's torch restatement against the numpy oracle, and the benchmark's row state.
+
+The benchmark times ``oracle/torch_cpu.py`` on a sample of its own serving state. These tests
+check (1) that the torch restatement computes what the numpy oracle computes (decode attention
+with sink, H2O scores, the boundary's selection, relocation and repack), and (2) that the
+benchmark's pre-compacted rows, renumbered onto a local pool as the baseline does it, are valid
+boundary inputs at every length the workload draws (16K-64K plus its steps): the oracle's
+ownership and sliding-window guards (R:477-489) accept them.
+"""
+import numpy as np
+import pytest
+import torch
+
+import bench
+import oracle as O
+from oracle import torch_cpu as TC
+
+HQ, G, D = 64, 8, 64
+
+
+def test_decode_layer_matches_oracle():
+    g = torch.Generator().manual_seed(0)
+    slots = 700
+    k = torch.randn((slots, G, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((slots, G, D), generator=g).to(torch.bfloat16)
+    q = torch.randn((HQ, D), generator=g)
+    sinks = torch.randn(HQ, generator=g)
+    csr = torch.randperm(slots - 1, generator=g)[:523] + 1
+    for mode in (1, 2):
+        sc = torch.zeros((G, slots))
+        o = TC.decode_layer(q, k, v, csr, sinks, 0.125, sc, mode)
+        want_o, norm = O.decode_attention(q.numpy(), k.float().numpy(), v.float().numpy(), csr.numpy(),
+                                          sinks.numpy(), 0.125)
+        want = np.zeros((G, slots))
+        O.decode_scores_into(want, q.numpy(), k.float().numpy(), csr.numpy(), norm, 0.125, mode)
+        np.testing.assert_allclose(o.numpy(), want_o, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(sc.numpy(), want, rtol=1e-4, atol=1e-7)
+
+
+def _row(n, interval, budget, prefix, recent, layers, seed):
+    """The benchmark's pre-compacted row at length n over a fresh random slot order."""
+    g = torch.Generator().manual_seed(seed)
+    slots = torch.randperm(4 * n, generator=g)[:n + 64] + 1
+
+    def middle(lo, hi, mid):
+        draw = torch.rand((layers * G, hi - lo), generator=g)
+        return (draw.argsort(-1)[:, :mid].sort(-1).values + lo).view(layers, G, mid)
+
+    return bench.precompacted_row(n, interval, budget, prefix, recent, slots, n + 64, middle)
+
+
+def _oracle_state(ls, layers, seed):
+    rng = np.random.default_rng(seed)
+    m = ls["used"].numel() + 1
+    keys = [rng.standard_normal((m, G, D)).astype(np.float32) for _ in range(layers)]
+    values = [rng.standard_normal((m, G, D)).astype(np.float32) for _ in range(layers)]
+    scores = rng.random((layers, G, m)).astype(np.float32)
+    r2t = ls["req_to_token"].numpy()[None]
+    ost = O.OracleState(keys, values, r2t, scores)
+    ost.table[0, :ls["count"]] = ls["table"].numpy()
+    return ost
+
+
+def _boundary_both(ls, layers, budget, prefix, recent, cursor, seed):
+    """Run the numpy oracle and the torch restatement on the same local row; compare."""
+    n = ls["n"]
+    ost = _oracle_state(ls, layers, seed)
+    kp = [torch.from_numpy(k.copy()) for k in ost.keys]
+    vp = [torch.from_numpy(v.copy()) for v in ost.values]
+    sc = torch.from_numpy(ost.scores.copy())
+    table = torch.from_numpy(ost.table[0].copy())
+    r2t = torch.from_numpy(ost.req_to_token[0].copy())
+    cfg = {"name": "head_sum_2048", "budget": budget, "prefix": prefix, "recent": recent, "seed": 0}
+    oe = O.live_entry(cfg)
+    oe.update(frontier=ls["frontier"], count=ls["count"])
+    if ls["count"]:
+        oe["pos"] = ls["pos"].numpy()
+    leftover = O.boundary(ost, 0, oe, n, cursor, free=lambda s: None)
+    out = TC.boundary(kp, vp, sc, table, r2t, ls["pos"], ls["count"], ls["frontier"], n, budget, prefix, recent,
+                      cursor)
+    if leftover is None:
+        assert out is None
+        return False
+    count, pos, left = out
+    assert count == oe["count"]
+    assert np.array_equal(pos.numpy(), oe["pos"])
+    assert np.array_equal(left.numpy(), leftover)
+    assert np.array_equal(table[:count].numpy(), ost.table[0, :count])
+    assert np.array_equal(r2t.numpy(), ost.req_to_token[0])
+    assert np.array_equal(sc.numpy(), ost.scores)
+    for l in range(layers):
+        assert np.array_equal(kp[l].numpy(), ost.keys[l])
+        assert np.array_equal(vp[l].numpy(), ost.values[l])
+    return True
+
+
+def test_boundary_matches_oracle_small():
+    """Small rows, fresh (count 0) and pre-compacted, with and without a cursor."""
+    for seed, (n, cursor) in enumerate([(1300, None), (1300, 1250), (2100, None), (2100, 2050), (2047, 1990)]):
+        row = _row(n, 64, 512, 64, 128, 2, seed)
+        ls = bench.local_row_state(row["req_to_token"] if row["table"] is None else row["table"],
+                                   row["req_to_token"], row["pos"], row["count"], row["frontier"], n)
+        assert _boundary_both(ls, 2, 512, 64, 128, cursor, seed)
+
+
+@pytest.mark.parametrize("n", [32768 + 65, 35580, 36801, 44029, 52001, 65536 + 600])
+def test_benchmark_rows_are_valid_boundary_inputs(n):
+    """The benchmark's rows at its own budget (32768 = 512 + 4096 + 28160), interval 64 and
+    cursor n - 256, renumbered as the CPU baseline renumbers them: the oracle's guards accept
+    them and the torch restatement agrees with it (n = 35580, f = 35520 is the row whose
+    recent-window slots were once missing from the baseline's state)."""
+    budget, prefix, recent = 32768, 512, 4096
+    row = _row(n, 64, budget, prefix, recent, 1, n)
+    assert row["count"] == budget
+    ls = bench.local_row_state(row["table"], row["req_to_token"], row["pos"], row["count"], row["frontier"], n)
+    # Every slot the row holds is in the local pool, and the recent window's real slots are there.
+    assert ls["used"].numel() == budget + n - row["frontier"]
+    assert (ls["req_to_token"][row["frontier"] - recent:n] > 0).all()
+    assert _boundary_both(ls, 1, budget, prefix, recent, n - 256, n)
