@@ -182,6 +182,7 @@ class Workload:
         width = -(-width // 256) * 256
         # Pools: 12 full layers, random N(0, 1) bf16 with planted heavy hitters per KV head.
         keys, values = {}, {}
+        self.dup_pairs = {}  # layer -> (dst, src): slot dst's key row (all heads) copied from src
         for l in range(L):
             k = torch.randn((slots, HKV, D), device=dev, dtype=torch.bfloat16)
             v = torch.randn((slots, HKV, D), device=dev, dtype=torch.bfloat16)
@@ -198,6 +199,7 @@ class Workload:
                 dst = torch.randperm(slots - 1, device=dev, generator=gen)[:nd] + 1
                 src = torch.randint(1, slots, (nd,), device=dev, generator=gen)
                 k[dst] = k[src]
+                self.dup_pairs[l] = (dst, src)
             keys[l], values[l] = k, v
         pool = SimpleNamespace(layers_mapping={l: (l, False) for l in range(L)},
                                get_key_buffer=keys.__getitem__, get_value_buffer=values.__getitem__)
@@ -211,6 +213,10 @@ class Workload:
         st.score_mode = "eager" if args.eager else "queue"
         self.st = st
         st.scores.uniform_(0.0, 1.0, generator=torch.Generator(device=dev).manual_seed(7))
+        # A duplicated key starts with its source's scores (copied as the keys were, all sources
+        # read first): the two stay exactly tied through every score update that sees both.
+        for l, (dst, src) in self.dup_pairs.items():
+            st.scores[l][:, dst] = st.scores[l][:, src]
         r2t = torch.zeros((bs + 1, width), dtype=torch.int32)
         table = torch.zeros((bs + 1, width), dtype=torch.int32)
         self.entries = []
@@ -497,6 +503,95 @@ def copy_calibration(torch, mib):
 PEAK_BF16_TFLOPS = 2500.0
 
 
+class PrefillWorkload:
+    """The chunked-prefill workload at the 79,720-token shape: 12 full layers of random bf16 keys
+    (5 % planted heavy hitters) and values, one row whose prompt fills 79,720 slots in random
+    order, one 8192-query block of random queries (each chunk takes its first ``count``), the
+    row's policy config (budget 512 + 4096 + 24,064; block policies: layer-shared blocks)."""
+
+    PROMPT, CHUNK, CAP = 79720, 8192, 512 + 4096 + 24064
+
+    def __init__(self, args, torch, ge):
+        self.args, self.torch, self.ge = args, torch, ge
+        prompt, chunk = self.PROMPT, self.CHUNK
+        L = self.layers = args.layers
+        slots = prompt + 64
+        g = torch.Generator(device="cuda").manual_seed(args.seed)
+        keys, values = {}, {}
+        for l in range(L):
+            k = torch.randn((slots + 1, HKV, D), device="cuda", dtype=torch.bfloat16, generator=g)
+            u = torch.randn((HKV, D), device="cuda", generator=g)
+            u = u / u.norm(dim=-1, keepdim=True)
+            heavy = torch.rand((slots + 1, HKV), device="cuda", generator=g) < 0.05
+            planted = (4 * k.float().norm(dim=-1, keepdim=True) * u[None]).to(torch.bfloat16)
+            keys[l] = torch.where(heavy[..., None], planted, k)
+            values[l] = torch.randn((slots + 1, HKV, D), device="cuda", dtype=torch.bfloat16, generator=g)
+        self.keys, self.values = keys, values
+        pool = SimpleNamespace(layers_mapping={l: (l, False) for l in range(L)},
+                               get_key_buffer=keys.__getitem__, get_value_buffer=values.__getitem__)
+        width = -(-prompt // 256) * 256
+        self.backend = SimpleNamespace(
+            token_to_kv_pool=pool, max_kv_splits=16,
+            req_to_token_pool=SimpleNamespace(req_to_token=torch.zeros((2, width), dtype=torch.int32, device="cuda")),
+            kv_indptr=torch.zeros(3, dtype=torch.int32, device="cuda"))
+        ge.STATE = None
+        st = self.st = ge.state(self.backend)
+        self.q = torch.randn((chunk, HQ, D), device="cuda", dtype=torch.bfloat16, generator=g)
+        self.sinks = torch.randn(HQ, device="cuda", generator=g)
+        st.req_to_token[1, :prompt] = (torch.randperm(slots, device="cuda", generator=g)[:prompt] + 1).int()
+        self.layer_objs = [SimpleNamespace(sliding_window_size=-1, tp_q_head_num=HQ, tp_k_head_num=HKV,
+                                           qk_head_dim=D, layer_id=l, scaling=D ** -0.5) for l in range(L)]
+        self.cfg = {"name": args.prefill_policy, "budget": self.CAP, "prefix": 512, "recent": 4096,
+                    "seed": args.seed}
+        self.block_policy = args.prefill_policy in ("block_sum_2048", "block_max_2048")
+        if self.block_policy:
+            self.cfg.update(block=args.prefill_block, shared=True, score_delay=args.prefill_delay,
+                            max_evicted_blocks=args.prefill_cap)
+        self.starts = list(range(0, prompt, chunk))
+
+    def run(self, timing=None, observe=None):
+        """One pass over the prompt from a fresh row (no eviction state, zero scores; the pools
+        keep whatever earlier passes moved): before each chunk after the first, the row's
+        boundary (replay mode: survivors relocated, nothing freed); then the chunk's prefill
+        scores on every layer. ``timing`` collects event pairs per chunk ("boundary", "score");
+        ``observe(stage, start, entry)`` runs before ("before") and after ("after") each boundary.
+        Returns the entry and the resident prefix length of each chunk."""
+        torch, ge, st = self.torch, self.ge, self.st
+        st.table.zero_()
+        st.count.zero_()
+        st.frontier.zero_()
+        st.scores.zero_()
+        entry = ge._live_entry(SimpleNamespace(rid="prompt", session=None), self.cfg, "replay")
+        if entry["error"]:
+            raise ValueError(f"--prefill config: {entry['error']}")
+        st.entries[1] = entry
+        word = ge.requests.score_word(entry)  # score mode and delay
+        st.mode[1] = word
+        resident = []
+        for start in self.starts:
+            count = min(self.CHUNK, self.PROMPT - start)
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            ev[0].record()
+            if start:
+                if observe:
+                    observe("before", start, entry)
+                ge._boundary(st, 1, entry, start)
+                if observe:
+                    observe("after", start, entry)
+            ev[1].record()
+            prefix = torch.cat((st.table[1, :entry["count"]], st.req_to_token[1, entry["frontier"]:start]))
+            new = st.req_to_token[1, start:start + count]
+            for l in range(self.layers):
+                ge._prefill_scores(st, l, word, self.layer_objs[l], self.q[:count], self.keys[l], self.sinks,
+                                   prefix, new)
+            ev[2].record()
+            resident.append(prefix.numel())
+            if timing is not None:
+                timing["boundary"].append(ev[:2])
+                timing["score"].append(ev[1:])
+        return entry, resident
+
+
 def prefill_bench(args, torch, ge):
     """Chunked prefill at the 79,720-token shape with eviction: one row prefills 8192-token
     chunks; before each chunk the row's boundary keeps 512 + 4096 + 24,064 positions with the
@@ -507,79 +602,18 @@ def prefill_bench(args, torch, ge):
     Scoring work = 2 * 64 heads * 64 dims flop per causal (query, key) pair for one QK^T pass
     (the kernel issues a second pass: the normaliser first, then the probabilities). Boundaries
     run in replay mode (survivors relocated, nothing freed) and are timed separately."""
-    prompt, chunk, cap = 79720, 8192, 512 + 4096 + 24064
-    L = args.layers
-    slots = prompt + 64
-    g = torch.Generator(device="cuda").manual_seed(args.seed)
-    keys, values = {}, {}
-    for l in range(L):
-        k = torch.randn((slots + 1, HKV, D), device="cuda", dtype=torch.bfloat16, generator=g)
-        u = torch.randn((HKV, D), device="cuda", generator=g)
-        u = u / u.norm(dim=-1, keepdim=True)
-        heavy = torch.rand((slots + 1, HKV), device="cuda", generator=g) < 0.05
-        planted = (4 * k.float().norm(dim=-1, keepdim=True) * u[None]).to(torch.bfloat16)
-        keys[l] = torch.where(heavy[..., None], planted, k)
-        values[l] = torch.randn((slots + 1, HKV, D), device="cuda", dtype=torch.bfloat16, generator=g)
-    pool = SimpleNamespace(layers_mapping={l: (l, False) for l in range(L)},
-                           get_key_buffer=keys.__getitem__, get_value_buffer=values.__getitem__)
-    width = -(-prompt // 256) * 256
-    backend = SimpleNamespace(token_to_kv_pool=pool, max_kv_splits=16,
-                              req_to_token_pool=SimpleNamespace(req_to_token=torch.zeros((2, width), dtype=torch.int32,
-                                                                                         device="cuda")),
-                              kv_indptr=torch.zeros(3, dtype=torch.int32, device="cuda"))
-    ge.STATE = None
-    st = ge.state(backend)
-    q = torch.randn((chunk, HQ, D), device="cuda", dtype=torch.bfloat16, generator=g)
-    sinks = torch.randn(HQ, device="cuda", generator=g)
-    st.req_to_token[1, :prompt] = (torch.randperm(slots, device="cuda", generator=g)[:prompt] + 1).int()
-    layer_objs = [SimpleNamespace(sliding_window_size=-1, tp_q_head_num=HQ, tp_k_head_num=HKV, qk_head_dim=D,
-                                  layer_id=l, scaling=D ** -0.5) for l in range(L)]
-    cfg = {"name": args.prefill_policy, "budget": cap, "prefix": 512, "recent": 4096, "seed": args.seed}
-    block_policy = args.prefill_policy in ("block_sum_2048", "block_max_2048")
-    if block_policy:
-        cfg.update(block=args.prefill_block, shared=True, score_delay=args.prefill_delay,
-                   max_evicted_blocks=args.prefill_cap)
-    starts = list(range(0, prompt, chunk))
+    w = PrefillWorkload(args, torch, ge)
+    prompt, chunk, cap, L, starts = w.PROMPT, w.CHUNK, w.CAP, w.layers, w.starts
+    block_policy = w.block_policy
     timing = {"score": [], "boundary": []}
 
-    def run(record):
-        # A fresh row: no eviction state, zero scores; the pools keep whatever earlier runs moved.
-        st.table.zero_()
-        st.count.zero_()
-        st.frontier.zero_()
-        st.scores.zero_()
-        entry = ge._live_entry(SimpleNamespace(rid="prompt", session=None), cfg, "replay")
-        if entry["error"]:
-            raise ValueError(f"--prefill config: {entry['error']}")
-        st.entries[1] = entry
-        word = ge.requests.score_word(entry)  # score mode and delay
-        st.mode[1] = word
-        resident = []
-        for start in starts:
-            count = min(chunk, prompt - start)
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-            ev[0].record()
-            if start:
-                ge._boundary(st, 1, entry, start)
-            ev[1].record()
-            prefix = torch.cat((st.table[1, :entry["count"]], st.req_to_token[1, entry["frontier"]:start]))
-            new = st.req_to_token[1, start:start + count]
-            for l in range(L):
-                ge._prefill_scores(st, l, word, layer_objs[l], q[:count], keys[l], sinks, prefix, new)
-            ev[2].record()
-            resident.append(prefix.numel())
-            if record:
-                timing["boundary"].append(ev[:2])
-                timing["score"].append(ev[1:])
-        return entry, resident
-
-    run(False)
+    w.run()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     reps = max(1, min(args.steps, 3))  # one step is the whole 79,720-token prompt (about a second)
     start.record()
     for _ in range(reps):
-        entry, resident = run(True)
+        entry, resident = w.run(timing)
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / reps

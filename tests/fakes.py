@@ -1,7 +1,11 @@
-"""Fake SGLang objects for driving the runtime hooks, after the reference test's fakes (T:19-39)."""
+"""Fake SGLang objects for driving the runtime hooks, after the reference test's fakes (T:19-39),
+and the oracle-side mirror of a fake backend's state."""
 from types import SimpleNamespace
 
+import numpy as np
 import torch
+
+import oracle as O
 
 FULL = (1, 3)
 
@@ -36,3 +40,24 @@ def entry(ge, name, budget, prefix, recent, seed, kind="live", record=False):
 def layer(layer_id, heads=64, kv_heads=8, dim=64, scaling=0.125):
     return SimpleNamespace(sliding_window_size=-1, tp_q_head_num=heads, tp_k_head_num=kv_heads,
                            qk_head_dim=dim, layer_id=layer_id, scaling=scaling)
+
+
+def oracle_state(b, st, full=FULL):
+    """The oracle's copy of the backend's full-layer pools, req_to_token and scores."""
+    keys = [b.token_to_kv_pool.get_key_buffer(l).float().cpu().numpy() for l in full]
+    values = [b.token_to_kv_pool.get_value_buffer(l).float().cpu().numpy() for l in full]
+    return O.OracleState(keys, values, st.req_to_token.cpu().numpy(), st.scores.cpu().numpy())
+
+
+def assert_same_state(b, st, ost, e, oe, row, n_rows, full=FULL):
+    """After the same boundary on the GPU and in the oracle: entries, table, counts, retained
+    positions, req_to_token of the first n_rows rows, scores and pools are identical."""
+    assert e["count"] == oe["count"] and e["frontier"] == oe["frontier"]
+    assert np.array_equal(st.table[row, :e["count"]].cpu().numpy(), ost.table[row, :oe["count"]])
+    assert int(st.count[row]) == e["count"] and int(st.frontier[row]) == e["frontier"]
+    assert np.array_equal(e["pos"].cpu().numpy(), oe["pos"])
+    assert np.array_equal(st.req_to_token[:n_rows].cpu().numpy(), ost.req_to_token[:n_rows])
+    assert np.array_equal(st.scores.cpu().numpy(), ost.scores)
+    for index, l in enumerate(full):
+        assert np.array_equal(b.token_to_kv_pool.get_key_buffer(l).float().cpu().numpy(), ost.keys[index])
+        assert np.array_equal(b.token_to_kv_pool.get_value_buffer(l).float().cpu().numpy(), ost.values[index])

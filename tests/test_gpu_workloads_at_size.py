@@ -1,0 +1,338 @@
+"""Parity at the benchmark workloads' own sizes, through the C ABI, against the oracle.
+
+* Decode at 32,768 resident keys (bs 1, one layer): attention output and the step's scores.
+* Decode inside the bs=32 workload (12 layers, 16K-64K tokens, budget 32,768): output and scores
+  of three sequences (smallest, median and largest resident set) on the first and last layer.
+* Eviction at every step (8 sequences at 128K, budget 32,768, 10 % duplicate keys whose scores
+  stay exactly tied): every row's kept positions per (layer, KV head) equal the oracle's
+  ``choose`` on the GPU's own flushed scores, for three consecutive steps, and the new tables'
+  slots hold the claimed positions' K, V and scores.
+* Selection with exact ties at the cut on 32K-column rows (coarse scores), on both the
+  LDS-resident and the larger-row selection paths.
+* Chunked prefill at the 79,720-token shape: the last 256 queries of an 8192-query chunk over a
+  28,672-key prefix against the oracle's update; the probability mass of a whole 8192-query
+  chunk over that prefix; and the real multi-chunk flow with 16-token layer-shared block
+  eviction, whose every boundary keeps the oracle's ``choose_blocks`` set on the GPU's scores.
+"""
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from fakes import allocator, assert_same_state, backend, layer, oracle_state
+
+pytestmark = pytest.mark.gpu
+
+G, D = 8, 64
+
+
+@pytest.fixture(autouse=True)
+def ge():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    import gstar_evict
+    gstar_evict.STATE = None
+    yield gstar_evict
+    gstar_evict.STATE = None
+    torch.cuda.empty_cache()
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+# --------------------------------------------------------------------------
+# Decode
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("mode,queued", [(1, True), (2, False)])
+def test_decode_at_32k_resident_keys(ge, mode, queued):
+    n = 32768
+    _say(f"decode at {n} resident, mode {mode}, queued {queued}")
+    g = torch.Generator().manual_seed(40 + mode)
+    b = backend(rows=2, width=n + 256, slots=n + 4096, gen=g)
+    st = ge.state(b)
+    st.score_mode = "queue" if queued else "eager"
+    st.mode[1] = mode
+    perm = (torch.randperm(n + 4095, generator=g)[:n] + 1).int().cuda()
+    st.req_to_token[1, :n] = perm
+    q = torch.randn((1, 64, D), generator=g).to(torch.bfloat16).cuda()
+    sinks = torch.randn(64, generator=g).to(torch.bfloat16).cuda()
+    rows = torch.tensor([1], device="cuda")
+    kv_indices = torch.zeros(n, dtype=torch.int32, device="cuda")
+    ge.fill(b, 1, torch.tensor([n], device="cuda"), rows, kv_indices)
+    assert torch.equal(kv_indices, perm)
+    b.forward_metadata = SimpleNamespace(kv_indptr=b.kv_indptr[:2], kv_indices=kv_indices)
+    fb = SimpleNamespace(out_cache_loc=torch.zeros(1, dtype=torch.int64, device="cuda"), req_pool_indices=rows,
+                         seq_lens_cpu=torch.tensor([n]))
+    o = torch.empty_like(q)
+    assert ge.decode(b, q.view(1, -1), layer(1), fb, sinks, o.view(1, -1))
+    ge.flush(st)
+    torch.cuda.synchronize()
+    keys = b.token_to_kv_pool.get_key_buffer(1).float().cpu().numpy()
+    values = b.token_to_kv_pool.get_value_buffer(1).float().cpu().numpy()
+    qn, sl = q[0].float().cpu().numpy(), perm.cpu().numpy()
+    want_o, norm = O.decode_attention(qn, keys, values, sl, sinks.float().cpu().numpy(), 0.125)
+    got_o = o[0].float().cpu().numpy()
+    np.testing.assert_allclose(got_o, want_o, rtol=2e-2, atol=2e-2)  # bf16 output
+    assert np.abs(got_o - want_o).mean() < 2e-3
+    want = np.zeros((G, keys.shape[0]))
+    O.decode_scores_into(want, qn, keys, sl, norm, 0.125, mode)
+    np.testing.assert_allclose(st.scores[0].cpu().numpy(), want, rtol=2e-3, atol=1e-6)  # T:48-78
+
+
+def _row_list(st, e, row, n):
+    return torch.cat((st.table[row, :e["count"]], st.req_to_token[row, e["frontier"]:n])).long()
+
+
+def test_decode_outputs_and_scores_in_the_bs32_workload(ge):
+    import bench
+    args = bench.parse(["--steps", "4", "--warmup", "0", "--no-cpu-baseline"])
+    _say("bs=32 workload: building")
+    w = bench.Workload(args, torch, ge)
+    st, pool = w.st, w.backend.token_to_kv_pool
+    w.step(account=False)
+    ge.finish_boundaries(st)
+    ge.flush(st)
+    # Rows with no boundary due at the next step, so their lists only grow by the new token.
+    free = [i for i in range(args.bs)
+            if not (w.lens[i] % args.interval == 0 and w.lens[i] > w.entries[i]["last_boundary"])]
+    free.sort(key=w.resident)
+    sample = [free[0], free[len(free) // 2], free[-1]]
+    for i in sample:  # start their scores from zero: the test sees exactly one step's update
+        st.scores[:, :, _row_list(st, w.entries[i], i + 1, w.lens[i])] = 0.0
+    w.step(account=False)
+    ge.finish_boundaries(st)
+    ge.flush(st, [i + 1 for i in sample])
+    torch.cuda.synchronize()
+    for i in sample:
+        e, n = w.entries[i], w.lens[i]
+        slots = _row_list(st, e, i + 1, n)
+        local = np.arange(slots.numel())
+        _say(f"bs=32 workload: sequence {i}, {slots.numel()} resident keys")
+        for l in (0, args.layers - 1):
+            keys = pool.get_key_buffer(l)[slots].float().cpu().numpy()
+            values = pool.get_value_buffer(l)[slots].float().cpu().numpy()
+            qn = w.q[l][i].float().cpu().numpy()
+            want_o, norm = O.decode_attention(qn, keys, values, local, w.sinks[l].float().cpu().numpy(), D ** -0.5)
+            got_o = w.o[l][i].float().cpu().numpy()
+            np.testing.assert_allclose(got_o, want_o, rtol=2e-2, atol=2e-2)
+            assert np.abs(got_o - want_o).mean() < 2e-3
+            want = O.decode_score_update(qn, keys, local, norm, D ** -0.5, 1)
+            got = st.scores[l][:, slots].double().cpu().numpy()
+            np.testing.assert_allclose(got, want, rtol=2e-3, atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# Eviction at every step, 8 x 128K, exact ties
+# --------------------------------------------------------------------------
+
+def _claims_hold(st, pool, e, row, n, pos, k_before, v_before, scores_before, layers):
+    """The new table's slots hold, for every head, the K, V and score of the claimed position."""
+    table = st.table[row, :e["count"]].long()
+    heads = torch.arange(G, device="cuda")[:, None]
+    cols_n = pos.shape[-1]
+    for l in layers:
+        column_of = torch.full((G, n), -1, dtype=torch.int64, device="cuda")
+        column_of.scatter_(1, pos[l], torch.arange(cols_n, device="cuda").expand(G, -1).contiguous())
+        cols = column_of.gather(1, e["pos"][l].long())
+        assert bool((cols >= 0).all())
+        assert torch.equal(pool.get_key_buffer(l)[table].transpose(0, 1), k_before[l][cols, heads])
+        assert torch.equal(pool.get_value_buffer(l)[table].transpose(0, 1), v_before[l][cols, heads])
+        assert torch.equal(st.scores[l][:, table], scores_before[l].gather(1, cols))
+    assert table.unique().numel() == table.numel()
+
+
+def test_eviction_every_step_at_the_stress_shape(ge):
+    import bench
+    args = bench.parse(["--bs", "8", "--min-len", "131072", "--max-len", "131072", "--interval", "1",
+                        "--heavy", "0", "--dup", "0.1", "--steps", "6", "--warmup", "0", "--no-cpu-baseline"])
+    _say("stress workload: building")
+    w = bench.Workload(args, torch, ge)
+    st, pool = w.st, w.backend.token_to_kv_pool
+    L = args.layers
+    w.step(account=False)  # the rows start compacted at their length: the first boundary is one step on
+    ties = 0
+    for t in range(3):
+        ge.finish_boundaries(st)
+        ge.flush(st)  # each boundary flushes its row again and finds the queue empty
+        if t == 1:
+            # Coarse scores on one row: runs of exactly equal scores across the cut.
+            e = w.entries[3]
+            slots = _row_list(st, e, 4, w.lens[3])
+            coarse = torch.randint(0, 8, (L, G, slots.numel()), generator=torch.Generator().manual_seed(t))
+            st.scores[:, :, slots] = (coarse.float() / 8).cuda()
+        snaps = {}
+        for i in range(args.bs):
+            e, n = w.entries[i], w.lens[i]
+            slots = _row_list(st, e, i + 1, n)
+            pos = torch.empty((L, G, slots.numel()), dtype=torch.int64, device="cuda")
+            pos[..., :e["count"]] = e["pos"].long()
+            pos[..., e["count"]:] = torch.arange(e["frontier"], n, device="cuda")
+            scores = st.scores[:, :, slots].clone()
+            ties += slots.numel() - torch.unique(scores[0, 0]).numel()
+            snaps[i] = (n, slots, pos, scores)
+        checked = {i: ({l: pool.get_key_buffer(l)[snaps[i][1]].clone() for l in (0, L - 1)},
+                       {l: pool.get_value_buffer(l)[snaps[i][1]].clone() for l in (0, L - 1)}) for i in (0, 3)}
+        _say(f"stress workload: step {t}")
+        w.step(account=False)
+        ge.finish_boundaries(st)
+        torch.cuda.synchronize()
+        for i, (n, slots, pos, scores) in snaps.items():
+            e = w.entries[i]
+            assert e["frontier"] == n and e["count"] == args.budget, (t, i)
+            assert e["events"][-1]["boundary"] == n and e["events"][-1]["freed"] == 1
+            pos_np = pos.cpu().numpy()
+            keep, protected = O.choose("head_sum_2048", pos_np, n, args.budget, args.prefix, args.recent,
+                                       scores.double().cpu().numpy(), n - 256)
+            assert protected == args.prefix + args.recent
+            want = np.sort(np.take_along_axis(pos_np, keep, -1), -1)
+            got = np.sort(e["pos"].long().cpu().numpy(), -1)
+            assert np.array_equal(got, want), (t, i)
+            if i in checked:
+                _claims_hold(st, pool, e, i + 1, n, pos, checked[i][0], checked[i][1], scores, (0, L - 1))
+    assert ties > 0, "no exact score ties among the rows' candidates"
+
+
+@pytest.mark.parametrize("extra", [2048, 6000])
+def test_selection_with_ties_at_the_cut_on_32k_rows(ge, extra):
+    """Budget 32,768 (512 + 1024 + the rest scored) over 32,768 + extra candidates with 4 score
+    levels: thousands of exactly tied scores straddle the cut, which the newer position wins.
+    34,816 candidates keep the selection's keys in LDS; 38,768 take the larger-row path."""
+    budget, n = 32768, 32768 + extra
+    slots = n + 64
+    g = torch.Generator().manual_seed(extra)
+    b = backend(rows=2, width=n + 64, slots=slots, gen=g)
+    st = ge.state(b)
+    slot_of = (torch.randperm(slots - 1, generator=g)[:n] + 1).cuda()
+    st.req_to_token[1, :n] = slot_of.int()
+    st.scores[:, :, slot_of] = (torch.randint(0, 4, (2, G, n), generator=g).float() / 4).cuda()
+    ost = oracle_state(b, st)
+    cfg = {"name": "head_sum_2048", "budget": budget, "prefix": 512, "recent": 1024, "seed": 0}
+    e = ge._live_entry(SimpleNamespace(rid="r", session=None), cfg, "live")
+    oe = O.live_entry(dict(cfg))
+    freed, alloc = allocator(slots=slots)
+    ofreed = []
+    ge._boundary(st, 1, e, n, n - 128, alloc)
+    O.boundary(ost, 1, oe, n, n - 128, free=ofreed.append)
+    assert_same_state(b, st, ost, e, oe, 1, 2)
+    assert torch.cat(freed).cpu().numpy().tolist() == ofreed[0].tolist()
+
+
+# --------------------------------------------------------------------------
+# Chunked prefill at the 79,720-token shape
+# --------------------------------------------------------------------------
+
+def _prefill_case(ge, count, prefix_len, seed):
+    slots = prefix_len + count + 1024
+    g = torch.Generator().manual_seed(seed)
+    b = backend(rows=2, width=256, slots=slots, gen=g)
+    st = ge.state(b)
+    q = torch.randn((count, 64, D), generator=g).to(torch.bfloat16).cuda()
+    sinks = torch.randn(64, generator=g).to(torch.bfloat16).cuda()
+    perm = torch.randperm(slots - 1, generator=g)[:prefix_len + count] + 1
+    return b, st, q, sinks, perm[:prefix_len].cuda(), perm[prefix_len:].cuda()
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_prefill_scores_of_the_last_queries_over_a_28k_prefix(ge, mode):
+    """The last 256 queries of an 8192-query chunk whose prefix is 28,672 resident keys: 256
+    queries at CSR columns 36,608..36,863 over every earlier key."""
+    count, prefix_len = 256, 28672 + 8192 - 256
+    _say(f"prefill: {count} queries over {prefix_len} keys, mode {mode}")
+    b, st, q, sinks, prefix, new = _prefill_case(ge, count, prefix_len, seed=7 + mode)
+    keys = b.token_to_kv_pool.get_key_buffer(1)
+    before = torch.rand(st.scores.shape, generator=torch.Generator().manual_seed(3)).cuda()
+    st.scores.copy_(before)
+    ge._prefill_scores(st, 0, mode, layer(1), q, keys, sinks, prefix, new)
+    torch.cuda.synchronize()
+    kn, qn, sn = keys.float().cpu().numpy(), q.float().cpu().numpy(), sinks.float().cpu().numpy()
+    all_slots = torch.cat((prefix, new)).cpu().numpy()
+    upd = np.zeros((G, all_slots.size))
+    for lo in range(0, count, 32):  # the oracle in query blocks: query i sees columns <= prefix_len + i
+        hi = min(lo + 32, count)
+        part, _ = O.prefill_score_update(mode, qn[lo:hi], kn, sn, 0.125, G, all_slots[:prefix_len + lo],
+                                         all_slots[prefix_len + lo:prefix_len + hi])
+        upd[:, :prefix_len + hi] += part
+    expected = before.clone()
+    expected[0][:, torch.from_numpy(all_slots).cuda()] += torch.tensor(upd, dtype=torch.float32).cuda()
+    torch.testing.assert_close(st.scores, expected, rtol=1e-3, atol=1e-6)
+
+
+def test_prefill_mass_of_an_8k_chunk_over_a_28k_prefix(ge):
+    """Head-sum scores of a KV head add up to the non-sink probability mass of its 8 query heads
+    over all 8192 queries of the chunk (a size-independent check)."""
+    count, prefix_len = 8192, 28672
+    _say("prefill mass: 8192 queries over 28672 + 8192 keys")
+    b, st, q, sinks, prefix, new = _prefill_case(ge, count, prefix_len, seed=5)
+    keys = b.token_to_kv_pool.get_key_buffer(1)
+    st.scores.zero_()
+    ge._prefill_scores(st, 0, 1, layer(1), q, keys, sinks, prefix, new)
+    got = st.scores[0].double().sum(1).cpu()
+    kk = keys[torch.cat((prefix, new))].float().permute(1, 2, 0).contiguous()  # [G, D, T]
+    t = kk.shape[-1]
+    s = sinks.float().view(G, 8, 1)
+    total = torch.zeros(G, dtype=torch.float64)
+    for lo in range(0, count, 256):
+        hi = lo + 256
+        qq = q[lo:hi].float().view(hi - lo, G, 8, D).permute(1, 2, 0, 3).contiguous()  # [G, 8, q, D]
+        logits = torch.matmul(qq, kk[:, None]) * 0.125  # [G, 8, q, T]
+        qpos = prefix_len + torch.arange(lo, hi, device="cuda")
+        logits.masked_fill_(torch.arange(t, device="cuda")[None, None, None, :] > qpos[None, None, :, None], -torch.inf)
+        norm = torch.logaddexp(torch.logsumexp(logits, -1), s)
+        total += (1 - torch.exp(s - norm)).sum((1, 2)).double().cpu()
+    torch.testing.assert_close(got, total, rtol=1e-4, atol=1e-2)
+
+
+@pytest.mark.parametrize("variant", ["block16", "report"])
+def test_block_eviction_flow_of_the_79720_token_prompt(ge, variant):
+    """bench.py's --prefill flow (12 layers, 8192-token chunks, budget 512 + 4096 + 24,064): at
+    every boundary each layer keeps the oracle's ``choose_blocks`` set (one set for all KV heads)
+    computed from the GPU's own scores, and the relocated slots hold the claimed K, V, scores.
+    Variants: 16-token blocks (the default), and the reference report's ARC-AGI-3 settings
+    (4-token max blocks, score delay 128, at most 512 blocks evicted per boundary)."""
+    import bench
+    from gstar_evict.requests import boundary_budget
+    flags = ["--prefill", "--no-cpu-baseline"]
+    if variant == "report":
+        flags += ["--prefill-policy", "block_max_2048", "--prefill-block", "4", "--prefill-delay", "128",
+                  "--prefill-cap", "512"]
+    args = bench.parse(flags)
+    _say(f"prefill flow {variant}: building")
+    w = bench.PrefillWorkload(args, torch, ge)
+    st, pool, L = w.st, w.backend.token_to_kv_pool, w.layers
+    block = args.prefill_block
+    snap = {}
+    evicting = []
+
+    def observe(stage, start, entry):
+        if stage == "before":
+            slots = _row_list(st, entry, 1, start)
+            pos = torch.empty((L, G, slots.numel()), dtype=torch.int64, device="cuda")
+            if entry["count"]:
+                pos[..., :entry["count"]] = entry["pos"].long()
+            pos[..., entry["count"]:] = torch.arange(entry["frontier"], start, device="cuda")
+            snap.update(slots=slots, pos=pos, scores=st.scores[:, :, slots].clone(),
+                        k={l: pool.get_key_buffer(l)[slots].clone() for l in (0, L - 1)},
+                        v={l: pool.get_value_buffer(l)[slots].clone() for l in (0, L - 1)})
+            return
+        torch.cuda.synchronize()
+        n_cols = snap["slots"].numel()
+        if n_cols <= w.CAP:
+            return
+        _say(f"prefill flow {variant}: boundary at {start}, {n_cols} candidates")
+        pos_np = snap["pos"].cpu().numpy()
+        col = O.block_column_scores(snap["scores"].cpu().numpy(), pos_np, start, block, True,
+                                    args.prefill_policy == "block_max_2048")
+        keep, protected = O.choose_blocks(pos_np, start, boundary_budget(w.cfg, n_cols), 512, 4096, col, block)
+        want = np.sort(np.take_along_axis(pos_np, keep, -1), -1)
+        got = np.sort(entry["pos"].long().cpu().numpy(), -1)
+        assert np.array_equal(got, want), start
+        assert np.array_equal(got, np.broadcast_to(got[:, :1], got.shape))  # one set for a layer's heads
+        _claims_hold(st, pool, entry, 1, start, snap["pos"], snap["k"], snap["v"], snap["scores"], (0, L - 1))
+        evicting.append(start)
+
+    w.run(observe=observe)
+    assert len(evicting) >= 5
