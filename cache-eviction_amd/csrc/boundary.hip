@@ -739,6 +739,10 @@ constexpr int COOP_GROUPS = 8;
 constexpr int COOP_SLEEP = 20;
 constexpr int COOP_SPIN_LIMIT = 1 << 18;
 constexpr int COOP_MAX_LAYERS = 128;  // pool pointer tables held in LDS
+// Set in the top barrier counter when the first phase's wait is abandoned: only while the count
+// is below its target (a compare-and-swap against the value last read), so every workgroup sees
+// either the completed count or the abort, never both, and none stores anything.
+constexpr uint32_t COOP_ABORT = 0x80000000u;
 
 
 struct BndArgs {
@@ -776,6 +780,10 @@ struct BndArgs {
   uint16_t* scratch_kv;
   float* scratch_sc;
   uint32_t* grid_arrivals;  // single-pass relocation: grid barrier counter (zeroed by prep)
+  int relocation;           // GSE_RELOCATION_* the host planned (written to the status)
+  int coop_spin_limit;      // polls before a barrier wait gives up
+  uint32_t coop_extra_target;  // added to the first barrier's target (0; a test sets 1 to force the abort)
+  int fallback_only;        // relocate_rows_kernel: run only if the single pass was abandoned
 };
 
 // slots[c] = table[row, c] for c < count, else req_to_token[row, frontier + c - count] (R:428).
@@ -838,6 +846,7 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
     st.packed = 0;
     st.min_protected = mn;
     st.max_protected = mx;
+    st.relocation = a.relocation;
     *a.status = st;
   }
   __syncthreads();
@@ -943,6 +952,12 @@ template <int DIR>
 __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
   const gse_boundary_status st = *a.status;
   if (st.state != GSE_BOUNDARY_EVICTED || st.width <= 0) return;
+  if (a.fallback_only) {
+    // Behind the single pass: move the rows only if it was abandoned before any store.
+    if (!(__hip_atomic_load(a.grid_arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & COOP_ABORT)) return;
+    if (DIR == 0 && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+      a.status->relocation = GSE_RELOCATION_SCRATCH;
+  }
   const int64_t width = st.width;
   const int l = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -952,10 +967,13 @@ __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
   auto V = as_global(static_cast<uint16_t*>(a.v_pools[l]));
   const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
   float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
-  const int64_t j0 = (int64_t(blockIdx.x) * 4 + wave) * ROWS_PER_WAVE;
   // Scratch entry (l, j): K row (8 heads x 64) then V row, bf16; score row (8 heads).
   auto sk = [&](int64_t j) { return a.scratch_kv + ((int64_t(l) * a.budget + j) * 2) * (8 * 64) + 64 * g + 8 * piece; };
   auto ss = [&](int64_t j) { return a.scratch_sc + (int64_t(l) * a.budget + j) * 8 + g; };
+  // Blocks of 4 * ROWS_PER_WAVE entries, strided over the grid (one block each when the grid
+  // covers the budget; the fallback launch uses a small grid).
+  for (int64_t jb = blockIdx.x; jb * 4 * ROWS_PER_WAVE < width; jb += gridDim.x) {
+  const int64_t j0 = (jb * 4 + wave) * ROWS_PER_WAVE;
   if (DIR == 0) {
     int64_t src[ROWS_PER_WAVE];
 #pragma unroll
@@ -998,6 +1016,7 @@ __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
       if (piece == 0) srow[dst[r] * a.sss] = sc[r];
     }
   }
+  }
 }
 
 // Single-pass relocation for 8 KV heads x 64 dims, launched with no more workgroups than the
@@ -1011,7 +1030,11 @@ __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
 // its HBM traffic, and the next pool's loads are in flight while the barrier completes (each
 // pool is written in exactly one phase, so loads of a later phase never meet a store of an
 // earlier one). A barrier's wait is bounded: past 2^18 polls (about 0.3 s) a workgroup stops
-// waiting, marks the boundary GSE_BOUNDARY_ERR_RELOCATE, which the host raises, and waits no more.
+// waiting. In the first phase nothing has been stored: the waiting workgroup abandons the single
+// pass (COOP_ABORT), every workgroup returns without a store, and relocate_rows_kernel, launched
+// behind it in fallback mode, moves the rows through scratch. Once every workgroup has arrived at
+// the first barrier all of them are resident, so a later wait cannot outlast the limit in
+// practice; if one did, it marks the boundary GSE_BOUNDARY_ERR_RELOCATE, which the host raises.
 
 // The wave's loaded registers are in use here: the compiler waits for exactly these loads.
 GSE_DEVICE void landed(const uint4& x) { asm volatile("" ::"v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w)); }
@@ -1035,24 +1058,49 @@ GSE_DEVICE void grid_arrive(BndArgs& a, uint32_t phase) {
 }
 
 // Wait until every workgroup has arrived at phase `phase` (thread 0 polls, sleeping 20 x 64
-// cycles between reads); `gave_up` (thread 0's) ends all waiting after a timeout.
-GSE_DEVICE void grid_wait(BndArgs& a, uint32_t phase, bool& gave_up) {
+// cycles between reads). Returns false in every thread when the first phase was abandoned: past
+// the spin limit, thread 0 sets COOP_ABORT with a compare-and-swap against the count it last read
+// (an arrival since then fails the swap, and the wait goes on), so the abort can only land while
+// the count is below its target, and a workgroup that finds the count complete knows that no one
+// abandoned it. Thread 0 hands its decision to the workgroup through LDS (`go`). In later phases
+// `gave_up` (thread 0's) ends all waiting after a timeout.
+GSE_DEVICE bool grid_wait(BndArgs& a, uint32_t phase, bool& gave_up, uint32_t* go) {
   if (threadIdx.x == 0 && !gave_up) {
     const uint32_t groups = gridDim.x < uint32_t(COOP_GROUPS) ? gridDim.x : uint32_t(COOP_GROUPS);
-    const uint32_t target = (phase + 1) * groups;
+    const uint32_t target = (phase + 1) * groups + (phase == 0 ? a.coop_extra_target : 0u);
+    uint32_t proceed = 1;
     int spins = 0;
-    while (__hip_atomic_load(a.grid_arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+    for (;;) {
+      uint32_t v = __hip_atomic_load(a.grid_arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (v & COOP_ABORT) {
+        proceed = 0;
+        break;
+      }
+      if (v >= target) break;
       __builtin_amdgcn_s_sleep(COOP_SLEEP);
-      if (++spins > COOP_SPIN_LIMIT) {
+      if (++spins <= a.coop_spin_limit) continue;
+      if (phase == 0) {
+        if (__hip_atomic_compare_exchange_strong(a.grid_arrivals, &v, v | COOP_ABORT, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+          proceed = 0;
+          break;
+        }
+        spins = 0;  // an arrival came in since v was read: wait another round
+      } else {
         atomicExch(&a.status->state, int32_t(GSE_BOUNDARY_ERR_RELOCATE));
         gave_up = true;
         break;
       }
     }
+    if (phase == 0) *go = proceed;
   }
+  // The LDS write must land before the barrier; the vector loads of the next phase stay in flight
+  // (lgkmcnt(0) only: vmcnt and expcnt at their maximum).
+  if (phase == 0) __builtin_amdgcn_s_waitcnt(0xc07f);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  return phase != 0 || *go != 0;
 }
 
 template <int PER>
@@ -1060,6 +1108,7 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
   // The pool pointers in LDS: their reads wait on the LDS counter, not on the vector memory
   // counter that the phase's loads and stores hold.
   __shared__ uint16_t* pools[2][COOP_MAX_LAYERS];
+  __shared__ uint32_t go;  // the first barrier's outcome (grid_wait)
   const gse_boundary_status st = *a.status;
   if (st.state != GSE_BOUNDARY_EVICTED || st.width <= 0) return;  // the same for every workgroup
   for (int i = threadIdx.x; i < a.layers; i += COOP_THREADS) {
@@ -1123,7 +1172,7 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
     grid_arrive(a, uint32_t(2 * l));
     load_v(l);
     if (l + 1 < a.layers) sources(l + 1);  // the V loads have taken their addresses
-    grid_wait(a, uint32_t(2 * l), gave_up);
+    if (!grid_wait(a, uint32_t(2 * l), gave_up, &go)) return;  // abandoned: nothing stored
     {
       auto K = as_global(pools[0][l]);
       float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
@@ -1138,7 +1187,7 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
     for (int r = 0; r < PER; ++r) landed(vd[r]);
     grid_arrive(a, uint32_t(2 * l + 1));
     if (l + 1 < a.layers) load_k(l + 1);
-    grid_wait(a, uint32_t(2 * l + 1), gave_up);
+    grid_wait(a, uint32_t(2 * l + 1), gave_up, &go);
     {
       auto V = as_global(pools[1][l]);
 #pragma unroll
@@ -1654,12 +1703,24 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
     hipLaunchKernelGGL(select_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), select_lds_bytes(a.nwords), s, a);
   if (int rc = gse_launch_check("boundary select")) return rc;
 
+  int coop_blocks = 0, coop_per = 0;
+  if (kv_heads == 8 && head_dim == 64 && layers <= COOP_MAX_LAYERS) coop_plan(budget, &coop_blocks, &coop_per);
+  b.relocation = coop_blocks > 0 ? GSE_RELOCATION_SINGLE_PASS : GSE_RELOCATION_SCRATCH;
+  b.coop_spin_limit = COOP_SPIN_LIMIT;
+  b.coop_extra_target = 0;
+  // GSE_RELOCATE_TEST_ABORT=1 (tests only): the first barrier's target is one past the grid, so
+  // its wait can never complete; after 256 polls the single pass is abandoned and the fallback
+  // moves the rows.
+  const char* test_abort = getenv("GSE_RELOCATE_TEST_ABORT");
+  if (test_abort && test_abort[0] == '1') {
+    b.coop_spin_limit = 256;
+    b.coop_extra_target = 1;
+  }
+
   const size_t col_lds = size_t(128 + 16) * 4 + size_t(b.nwords_cols) * 4 + 16;
   hipLaunchKernelGGL(columns_kernel, dim3(1), dim3(SEL_THREADS), col_lds, s, b);
   if (int rc = gse_launch_check("boundary columns")) return rc;
 
-  int coop_blocks = 0, coop_per = 0;
-  if (kv_heads == 8 && head_dim == 64 && layers <= COOP_MAX_LAYERS) coop_plan(budget, &coop_blocks, &coop_per);
   if (coop_blocks > 0) {
     // An ordinary launch of at most as many workgroups as the device holds at once: the stream's
     // earlier kernels have retired before it starts, so every workgroup is resident.
@@ -1670,6 +1731,15 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
     else
       hipLaunchKernelGGL(relocate_coop_kernel<8>, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), 0, s, b);
     if (int rc = gse_launch_check("boundary relocate")) return rc;
+    // The fallback: if the single pass was abandoned (nothing stored), gather and scatter through
+    // scratch; otherwise these return at once.
+    BndArgs fb = b;
+    fb.fallback_only = 1;
+    const dim3 fgrid(32, unsigned(layers));
+    hipLaunchKernelGGL(relocate_rows_kernel<0>, fgrid, dim3(256), 0, s, fb);
+    if (int rc = gse_launch_check("boundary fallback gather")) return rc;
+    hipLaunchKernelGGL(relocate_rows_kernel<1>, fgrid, dim3(256), 0, s, fb);
+    if (int rc = gse_launch_check("boundary fallback scatter")) return rc;
   } else if (kv_heads == 8 && head_dim == 64) {
     const dim3 rgrid(unsigned((budget + 4 * ROWS_PER_WAVE - 1) / (4 * ROWS_PER_WAVE)), unsigned(layers));
     hipLaunchKernelGGL(relocate_rows_kernel<0>, rgrid, dim3(256), 0, s, b);

@@ -22,6 +22,7 @@ POLICY_IDS = {"head_sum_2048": 1, "head_max_sum_2048": 2, "random_2048": 3,
               "random_reservoir_2048": 4, "prefix_sliding_2048": 5, "block_sum_2048": 6, "block_max_2048": 7}
 BOUNDARY_EVICTED, BOUNDARY_DEFERRED, BOUNDARY_ERR_HEADS, BOUNDARY_ERR_SWA, BOUNDARY_ERR_PACKED = 0, 2, 3, 4, 5
 BOUNDARY_ERR_RELOCATE = 6
+RELOCATION_SINGLE_PASS, RELOCATION_SCRATCH = 0, 1
 
 _p, _i, _l, _f, _d = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double
 

@@ -77,8 +77,18 @@ enum {
   GSE_BOUNDARY_ERR_HEADS = 3,      /* heads protect different counts (R:388-389)             */
   GSE_BOUNDARY_ERR_SWA = 4,        /* a leftover slot still holds a sliding-window entry (R:477-479) */
   GSE_BOUNDARY_ERR_PACKED = 5,     /* packed ownership overlaps the sliding-window region (R:487-489) */
-  GSE_BOUNDARY_ERR_RELOCATE = 6    /* the single-pass relocation's grid barrier timed out (its
-                                      workgroups were not all resident); no reference counterpart */
+  GSE_BOUNDARY_ERR_RELOCATE = 6    /* the single-pass relocation's grid barrier timed out after its
+                                      first phase (no reference counterpart; not seen in practice:
+                                      a wait that times out in the first phase abandons the single
+                                      pass before any store, and the relocation runs through scratch) */
+};
+
+/* gse_boundary_status.relocation: how the survivors' K/V/score rows were moved. */
+enum {
+  GSE_RELOCATION_SINGLE_PASS = 0,  /* one kernel with grid barriers, or no move needed            */
+  GSE_RELOCATION_SCRATCH = 1       /* through scratch: chosen by the host (widths past the single
+                                      pass's capacity, GSE_RELOCATE_SCRATCH=1) or taken after the
+                                      single pass found its workgroups not all resident           */
 };
 
 typedef struct {
@@ -90,6 +100,7 @@ typedef struct {
   int32_t packed;           /* owned slots packed at the start of req_to_token  */
   int32_t min_protected;    /* smallest per-head protected count                */
   int32_t max_protected;    /* largest per-head protected count                 */
+  int32_t relocation;       /* GSE_RELOCATION_*                                 */
 } gse_boundary_status;
 
 /* Library version (major * 10000 + minor * 100 + patch) and last error text. */
