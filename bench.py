@@ -295,12 +295,15 @@ class Workload:
         # this workload's interval.
         ge.finish_boundaries(st)
         self.account_decode()
+        due = []
         for i, e in enumerate(self.entries):
             n = self.lens[i]
             if n % a.interval == 0 and n > e["last_boundary"]:
-                ge._start_boundary(st, i + 1, e, n, n - 256, self.alloc)
+                due.append((i + 1, e, n, n - 256))
                 if account:
                     self.started.append((i, n))
+        if due:
+            ge._start_boundaries(st, due, self.alloc)
         # Allocate the new token's slot (SGLang's allocator), then the CSR for every full layer.
         t = self.step_index
         new = self.new_slots[t]

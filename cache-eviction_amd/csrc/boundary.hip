@@ -186,8 +186,237 @@ GSE_DEVICE void bitmap_prefix(const uint32_t* words, int nwords, int* blockpre, 
   __syncthreads();
 }
 
-// One workgroup per (full layer, KV head) row.
-__global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelArgs a) {
+
+// ------------------------------------------------------------- boundary batch --
+//
+// One set of launches evicts up to MAX_BATCH rows (their selection, column split, protected
+// positions and compaction; the relocation runs one row at a time, since its moves are held in
+// registers across a grid barrier). The arguments the rows share (BndCommon) and each row's own
+// (BndRow, about 100 bytes) are passed by value; a kernel rebuilds its row's full argument struct
+// (bnd_args, sel_args) from them and from the row's workspace layout (row_layout).
+constexpr int MAX_BATCH = 8;
+constexpr int COOP_GROUPS = 8;  // single-pass relocation: barrier arrival groups
+
+#define GSE_HD __host__ __device__ __forceinline__
+
+struct BndArgs {
+  int layers, kv_heads, head_dim;
+  int64_t N, n, budget;
+  int prefix_sliding;
+  int block;  // tokens per eviction block (the kept width is whole blocks)
+  const int32_t* table_in;  // read by prep only
+  int32_t* table;
+  int64_t table_stride;
+  const int32_t* r2t;
+  int64_t r2t_stride;
+  int32_t* frontier;
+  int32_t* count;
+  int row;
+  int64_t row_count, row_frontier;
+  const int32_t* pos_old;
+  int64_t pstride;
+  int32_t* slots;
+  int32_t* prot_count;
+  int32_t* prot_low;  // [LG] protected positions below the tail region (head 0's sets the layout)
+  int32_t* middle;  // [LG, budget] each head's j-th kept middle column (its slot: slots[column])
+  int32_t* prot_cols;
+  int32_t* targets;
+  int32_t* pos_new;
+  int64_t* leftover;
+  gse_boundary_status* status;
+  int nwords_cols;
+  // relocation
+  void* const* k_pools;
+  void* const* v_pools;
+  int64_t kv_ss, kv_sh;
+  float* scores;
+  int64_t ssl, ssg, sss;
+  uint16_t* scratch_kv;
+  float* scratch_sc;
+  uint32_t* grid_arrivals;  // single-pass relocation: grid barrier counter (zeroed by prep)
+  int relocation;           // GSE_RELOCATION_* the host planned (written to the status)
+  int coop_spin_limit;      // polls before a barrier wait gives up
+  uint32_t coop_extra_target;  // added to the first barrier's target (0; a test sets 1 to force the abort)
+  int fallback_only;        // relocate_rows_kernel: run only if the single pass was abandoned
+};
+
+struct BndCommon {
+  int layers, kv_heads, head_dim;
+  int policy, block, shared, prefix_sliding;
+  int64_t budget, prefix, recent, seed;
+  int32_t* table;
+  int64_t table_stride;
+  const int32_t* r2t;
+  int64_t r2t_stride;
+  int32_t* frontier;
+  int32_t* count;
+  void* const* k_pools;
+  void* const* v_pools;
+  int64_t kv_ss, kv_sh;
+  float* scores;
+  int64_t ssl, ssg, sss;
+  uint16_t* scratch_kv;  // relocation scratch, shared: the rows relocate one after another
+  float* scratch_sc;
+  int relocation, coop_spin_limit;
+  uint32_t coop_extra_target;
+};
+
+struct BndRow {
+  int32_t row, has_cursor;
+  int64_t N, n, count, frontier, cursor, pstride, tail_from;
+  const int32_t* pos_old;
+  const double* random_scores;  // random_2048's draws [L, G, N]
+  int32_t* pos_new;
+  int64_t* leftover;
+  gse_boundary_status* status;
+  char* ws;  // the row's workspace region (row_layout)
+};
+
+struct BndBatch {
+  BndCommon c;
+  int nrows;
+  BndRow r[MAX_BATCH];
+};
+
+GSE_HD int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+GSE_HD bool block_policy(int policy) { return policy == GSE_POLICY_BLOCK_SUM || policy == GSE_POLICY_BLOCK_MAX; }
+GSE_HD bool table_policy(int policy) { return policy == GSE_POLICY_HEAD_SUM || policy == GSE_POLICY_HEAD_MAX_SUM; }
+
+// Byte offsets in a row's workspace region. Block policies add the position-indexed scratch
+// ([LG, n] scores, [LG, ceil(n / block)] block scores, [LG, N] column scores).
+struct RowLayout {
+  int64_t arrivals, col32, bypos, bscore, colscore, slots, keys, posw, prot, middle, prot_cols, targets, total;
+};
+
+GSE_HD RowLayout row_layout(int layers, int kv_heads, int64_t N, int64_t n, int64_t budget, int policy, int block) {
+  const int64_t LG = int64_t(layers) * kv_heads;
+  const bool blk = block_policy(policy);
+  const int64_t nblocks = blk && block > 0 ? (n + block - 1) / block : 0;
+  RowLayout L;
+  int64_t o = 0;
+  L.arrivals = o; o += 256 * (1 + COOP_GROUPS);
+  L.col32 = o; o += table_policy(policy) ? align256(LG * N * 4) : 0;
+  L.bypos = o; o += blk ? align256(LG * n * 4) : 0;
+  L.bscore = o; o += blk ? align256(LG * nblocks * 8) : 0;
+  L.colscore = o; o += blk ? align256(LG * N * 8) : 0;
+  L.slots = o; o += align256(((N + 31) / 32) * 32 * 4);  // whole 32-column words
+  L.keys = o; o += align256(LG * N * 8);
+  L.posw = o; o += align256(LG * N * 4);
+  L.prot = o; o += align256(2 * LG * 4);  // protected counts, then the counts below the tail region
+  L.middle = o; o += align256(LG * budget * 4);
+  L.prot_cols = o; o += align256(budget * 4);
+  L.targets = o; o += align256(budget * 4);
+  L.total = o;
+  return L;
+}
+
+GSE_HD RowLayout row_layout(const BndCommon& c, const BndRow& r) {
+  return row_layout(c.layers, c.kv_heads, r.N, r.n, c.budget, c.policy, c.block);
+}
+
+// The full boundary arguments of one row.
+GSE_HD BndArgs bnd_args(const BndCommon& c, const BndRow& r) {
+  const RowLayout L = row_layout(c, r);
+  const int64_t LG = int64_t(c.layers) * c.kv_heads;
+  BndArgs a = {};
+  a.layers = c.layers;
+  a.kv_heads = c.kv_heads;
+  a.head_dim = c.head_dim;
+  a.N = r.N;
+  a.n = r.n;
+  a.budget = c.budget;
+  a.prefix_sliding = c.prefix_sliding;
+  a.block = c.block;
+  a.table_in = c.table;
+  a.table = c.table;
+  a.table_stride = c.table_stride;
+  a.r2t = c.r2t;
+  a.r2t_stride = c.r2t_stride;
+  a.frontier = c.frontier;
+  a.count = c.count;
+  a.row = r.row;
+  a.row_count = r.count;
+  a.row_frontier = r.frontier;
+  a.pos_old = r.pos_old;
+  a.pstride = r.pstride;
+  a.slots = reinterpret_cast<int32_t*>(r.ws + L.slots);
+  a.prot_count = reinterpret_cast<int32_t*>(r.ws + L.prot);
+  a.prot_low = a.prot_count + LG;
+  a.middle = reinterpret_cast<int32_t*>(r.ws + L.middle);
+  a.prot_cols = reinterpret_cast<int32_t*>(r.ws + L.prot_cols);
+  a.targets = reinterpret_cast<int32_t*>(r.ws + L.targets);
+  a.pos_new = r.pos_new;
+  a.leftover = r.leftover;
+  a.status = r.status;
+  a.nwords_cols = int((r.N + 31) / 32);
+  a.k_pools = c.k_pools;
+  a.v_pools = c.v_pools;
+  a.kv_ss = c.kv_ss;
+  a.kv_sh = c.kv_sh;
+  a.scores = c.scores;
+  a.ssl = c.ssl;
+  a.ssg = c.ssg;
+  a.sss = c.sss;
+  a.scratch_kv = c.scratch_kv;
+  a.scratch_sc = c.scratch_sc;
+  a.grid_arrivals = reinterpret_cast<uint32_t*>(r.ws + L.arrivals);
+  a.relocation = c.relocation;
+  a.coop_spin_limit = c.coop_spin_limit;
+  a.coop_extra_target = c.coop_extra_target;
+  a.fallback_only = 0;
+  return a;
+}
+
+// The selection arguments of one row (boundary mode).
+GSE_HD SelArgs sel_args(const BndCommon& c, const BndRow& r) {
+  const RowLayout L = row_layout(c, r);
+  const int64_t LG = int64_t(c.layers) * c.kv_heads;
+  SelArgs a = {};
+  a.src.pos_old = r.pos_old;
+  a.src.pstride = r.pstride;
+  a.src.count = r.count;
+  a.src.frontier = r.frontier;
+  a.src.policy = c.policy;
+  a.src.table_scores = c.scores;
+  a.src.ssl = c.ssl;
+  a.src.ssg = c.ssg;
+  a.src.sss = c.sss;
+  a.src.slots = reinterpret_cast<const int32_t*>(r.ws + L.slots);
+  a.src.random_scores = block_policy(c.policy) ? reinterpret_cast<const double*>(r.ws + L.colscore) : r.random_scores;
+  a.src.seed = c.seed;
+  a.src.column_scores = table_policy(c.policy) ? reinterpret_cast<const float*>(r.ws + L.col32) : nullptr;
+  a.layers = c.layers;
+  a.kv_heads = c.kv_heads;
+  a.n_cols = r.N;
+  a.n = r.n;
+  a.budget = c.budget;
+  a.prefix = c.prefix;
+  a.recent = c.recent;
+  a.cursor = r.cursor;
+  a.has_cursor = r.has_cursor;
+  a.prefix_sliding = c.prefix_sliding;
+  a.boundary_mode = 1;
+  a.block = c.block;
+  a.tail_from = r.tail_from;
+  a.keys = reinterpret_cast<uint64_t*>(r.ws + L.keys);
+  a.posw = reinterpret_cast<int32_t*>(r.ws + L.posw);
+  a.prot_count = reinterpret_cast<int32_t*>(r.ws + L.prot);
+  a.prot_low = a.prot_count + LG;
+  a.middle = reinterpret_cast<int32_t*>(r.ws + L.middle);
+  a.prot_cols = reinterpret_cast<int32_t*>(r.ws + L.prot_cols);
+  a.pos_new = r.pos_new;
+  a.nwords = int((r.n + 31) / 32);
+  return a;
+}
+
+GSE_DEVICE SelArgs select_args(const SelArgs& a, int) { return a; }
+GSE_DEVICE SelArgs select_args(const BndBatch& b, int i) { return sel_args(b.c, b.r[i]); }
+
+// One workgroup per (full layer, KV head) row: grid (rows, 1) for a public call, (rows, batch
+// rows) for a boundary batch.
+template <typename Src>
+__global__ __launch_bounds__(SEL_THREADS) void select_kernel(Src src) {
+  const SelArgs a = select_args(src, blockIdx.y);
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   int* tmp = reinterpret_cast<int*>(lds);             // 128 ints: scan scratch
   int* hist = tmp + 128;                               // 256 bins
@@ -492,7 +721,9 @@ GSE_DEVICE void protected_columns(const SelArgs& a, uint32_t* words, int* wpre, 
   }
 }
 
-__global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
+// Grid (layers * kv_heads + 1, batch rows).
+__global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
+  const SelArgs a = select_args(b, blockIdx.y);
   constexpr int KPT = SEL_LDS_KEYS / SEL_THREADS;  // columns per thread: c = tid + k * SEL_THREADS
   constexpr int BATCH = 17;                         // columns whose loads are issued together
   static_assert(KPT % BATCH == 0, "whole batches");
@@ -735,7 +966,6 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(SelArgs a) {
 // 1.3 TB/s). Polls sleep 20 x 64 cycles between reads.
 constexpr int COOP_THREADS = 1024;
 constexpr int COOP_WAVES = COOP_THREADS / 64;
-constexpr int COOP_GROUPS = 8;
 constexpr int COOP_SLEEP = 20;
 constexpr int COOP_SPIN_LIMIT = 1 << 18;
 constexpr int COOP_MAX_LAYERS = 128;  // pool pointer tables held in LDS
@@ -745,49 +975,12 @@ constexpr int COOP_MAX_LAYERS = 128;  // pool pointer tables held in LDS
 constexpr uint32_t COOP_ABORT = 0x80000000u;
 
 
-struct BndArgs {
-  int layers, kv_heads, head_dim;
-  int64_t N, n, budget;
-  int prefix_sliding;
-  int block;  // tokens per eviction block (the kept width is whole blocks)
-  const int32_t* table_in;  // read by prep only
-  int32_t* table;
-  int64_t table_stride;
-  const int32_t* r2t;
-  int64_t r2t_stride;
-  int32_t* frontier;
-  int32_t* count;
-  int row;
-  int64_t row_count, row_frontier;
-  const int32_t* pos_old;
-  int64_t pstride;
-  int32_t* slots;
-  int32_t* prot_count;
-  int32_t* prot_low;  // [LG] protected positions below the tail region (head 0's sets the layout)
-  int32_t* middle;  // [LG, budget] each head's j-th kept middle column (its slot: slots[column])
-  int32_t* prot_cols;
-  int32_t* targets;
-  int32_t* pos_new;
-  int64_t* leftover;
-  gse_boundary_status* status;
-  int nwords_cols;
-  // relocation
-  void* const* k_pools;
-  void* const* v_pools;
-  int64_t kv_ss, kv_sh;
-  float* scores;
-  int64_t ssl, ssg, sss;
-  uint16_t* scratch_kv;
-  float* scratch_sc;
-  uint32_t* grid_arrivals;  // single-pass relocation: grid barrier counter (zeroed by prep)
-  int relocation;           // GSE_RELOCATION_* the host planned (written to the status)
-  int coop_spin_limit;      // polls before a barrier wait gives up
-  uint32_t coop_extra_target;  // added to the first barrier's target (0; a test sets 1 to force the abort)
-  int fallback_only;        // relocate_rows_kernel: run only if the single pass was abandoned
-};
+
 
 // slots[c] = table[row, c] for c < count, else req_to_token[row, frontier + c - count] (R:428).
-__global__ void prep_slots_kernel(BndArgs a) {
+// Grid (ceil(max N / 256), batch rows).
+__global__ void prep_slots_kernel(BndBatch b) {
+  const BndArgs a = bnd_args(b.c, b.r[blockIdx.y]);
   const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (c == 0 && a.grid_arrivals)
     for (int k = 0; k <= COOP_GROUPS; ++k) a.grid_arrivals[64 * k] = 0;  // the top and group counters
@@ -800,7 +993,9 @@ __global__ void prep_slots_kernel(BndArgs a) {
 // unprotected columns into targets and leftover, write the new table row:
 // protected columns below the tail region (Q of them, by position), the width
 // targets, then the remaining protected columns (Q = P for the reference's policies).
-__global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndArgs a) {
+// One workgroup per batch row.
+__global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndBatch b) {
+  const BndArgs a = bnd_args(b.c, b.r[blockIdx.x]);
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   int* tmp = reinterpret_cast<int*>(lds);
   int* bc = tmp + 128;
@@ -1198,7 +1393,9 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
 
 // pos_new[l, g, i'] = pos(l, g, prot_cols[i]) for the protected columns of every head row, at
 // the table's layout: i' = i below Q, width + i past it.
-__global__ __launch_bounds__(256) void protected_pos_kernel(BndArgs a) {
+// Grid (layers * kv_heads, batch rows).
+__global__ __launch_bounds__(256) void protected_pos_kernel(BndBatch b) {
+  const BndArgs a = bnd_args(b.c, b.r[blockIdx.y]);
   const gse_boundary_status st = *a.status;
   if (st.state != GSE_BOUNDARY_EVICTED) return;
   const int lg = blockIdx.x;
@@ -1215,14 +1412,19 @@ __global__ __launch_bounds__(256) void protected_pos_kernel(BndArgs a) {
 // The table-score policies rank each (layer, head) row by its columns' scores. A slot keeps its
 // heads' scores together (one 32-byte row at 8 heads), so one thread per (layer, column) reads
 // the row once and writes each head's score into that head's contiguous column array, instead of
-// every head's selection gathering the same row for 4 of its bytes. Grid (ceil(N / 256), layers).
-__global__ void table_columns_kernel(const float* scores, int64_t ssl, int64_t ssg, int64_t sss,
-                                     const int32_t* slots, int kv_heads, int64_t N, float* out) {
+// every head's selection gathering the same row for 4 of its bytes. Grid (ceil(max N / 256),
+// layers, batch rows).
+__global__ void table_columns_kernel(BndBatch b) {
+  const BndRow& r = b.r[blockIdx.z];
   const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const int l = blockIdx.y;
-  if (c >= N) return;
-  const float* row = scores + int64_t(l) * ssl + int64_t(slots[c]) * sss;
-  for (int g = 0; g < kv_heads; ++g) out[(int64_t(l) * kv_heads + g) * N + c] = row[int64_t(g) * ssg];
+  if (c >= r.N) return;
+  const RowLayout L = row_layout(b.c, r);
+  const int32_t* slots = reinterpret_cast<const int32_t*>(r.ws + L.slots);
+  float* out = reinterpret_cast<float*>(r.ws + L.col32);
+  const int kv_heads = b.c.kv_heads;
+  const float* row = b.c.scores + int64_t(l) * b.c.ssl + int64_t(slots[c]) * b.c.sss;
+  for (int g = 0; g < kv_heads; ++g) out[(int64_t(l) * kv_heads + g) * r.N + c] = row[int64_t(g) * b.c.ssg];
 }
 
 // ------------------------------------------------------ block policy scores --
@@ -1316,14 +1518,53 @@ struct LiveArgs {
   uint32_t* bitmap;  // ceil(num_slots / 32) words
 };
 
-__global__ void swa_guard_kernel(LiveArgs a) {
+// A live-compaction batch: what its rows share, then each row's own.
+struct LiveCommon {
+  float* scores;
+  int layers, kv_heads;
+  int64_t ssl, ssg, sss;
+  const int32_t* table;
+  int64_t table_stride;
+  int32_t* r2t;
+  int64_t r2t_stride;
+  const void* swa;
+  int swa_dtype;
+  int64_t num_slots;
+};
+
+struct LiveRow {
+  int32_t row;
+  int64_t n, true_len;
+  const int64_t* leftover;
+  gse_boundary_status* status;
+  uint32_t* bitmap;
+};
+
+struct LiveBatch {
+  LiveCommon c;
+  int nrows;
+  LiveRow r[MAX_BATCH];
+};
+
+GSE_DEVICE LiveArgs live_args(const LiveBatch& b, int i) {
+  const LiveCommon& c = b.c;
+  const LiveRow& r = b.r[i];
+  return LiveArgs{c.scores, c.layers, c.kv_heads, c.ssl, c.ssg, c.sss, c.table, c.table_stride, c.r2t, c.r2t_stride,
+                  r.row, r.n, r.true_len, r.leftover, c.swa, c.swa_dtype, c.num_slots, r.status, r.bitmap};
+}
+
+// Grid (64, batch rows).
+__global__ void swa_guard_kernel(LiveBatch b) {
+  const LiveArgs a = live_args(b, blockIdx.y);
   if (a.status->state != GSE_BOUNDARY_EVICTED) return;
   const int64_t nl = a.status->leftover;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nl; i += int64_t(gridDim.x) * blockDim.x)
     if (load_index_dyn(a.swa, a.swa_dtype, a.leftover[i]) != 0) atomicExch(&a.status->state, GSE_BOUNDARY_ERR_SWA);
 }
 
-__global__ void zero_leftover_kernel(LiveArgs a) {
+// Grid (256, batch rows).
+__global__ void zero_leftover_kernel(LiveBatch b) {
+  const LiveArgs a = live_args(b, blockIdx.y);
   if (a.status->state != GSE_BOUNDARY_EVICTED) return;
   const int64_t nl = a.status->leftover;
   const int64_t total = nl * a.layers * a.kv_heads;
@@ -1342,8 +1583,10 @@ GSE_DEVICE void bitmap_clear(uint32_t* p) { __hip_atomic_store(p, 0u, __ATOMIC_R
 // the caller's workspace.
 constexpr int64_t REPACK_LDS_WORDS = 36864;
 
+// One workgroup per batch row.
 template <bool LDS_BITMAP>
-__global__ __launch_bounds__(SEL_THREADS) void repack_kernel(LiveArgs a) {
+__global__ __launch_bounds__(SEL_THREADS) void repack_kernel(LiveBatch b) {
+  const LiveArgs a = live_args(b, blockIdx.x);
   __shared__ int tmp[128 + 16];
   __shared__ uint32_t lbits[LDS_BITMAP ? REPACK_LDS_WORDS : 1];
   if (a.status->state != GSE_BOUNDARY_EVICTED) return;
@@ -1405,41 +1648,11 @@ using namespace gse;
 
 namespace {
 
-int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
-
-struct BndLayout {
-  int64_t slots, keys, posw, prot, middle, prot_cols, targets, skv, ssc, bypos, bscore, colscore, col32, arrivals,
-      total;
-};
-
-bool block_policy(int policy) { return policy == GSE_POLICY_BLOCK_SUM || policy == GSE_POLICY_BLOCK_MAX; }
-
-// Block policies add the position-indexed scratch ([LG, n] scores, [LG, ceil(n / block)] block
-// scores, [LG, N] column scores).
-BndLayout bnd_layout(int layers, int kv_heads, int head_dim, int64_t N, int64_t n, int64_t budget, int policy,
-                     int block) {
+// The relocation scratch at the start of a boundary workspace, shared by a batch's rows (they
+// relocate one after another on the stream): [L*G, budget] moved K/V rows and scores.
+int64_t scratch_bytes(int layers, int kv_heads, int head_dim, int64_t budget) {
   const int64_t LG = int64_t(layers) * kv_heads;
-  const bool blk = block_policy(policy);
-  const int64_t nblocks = blk && block > 0 ? (n + block - 1) / block : 0;
-  BndLayout L;
-  int64_t o = 0;
-  L.arrivals = o; o += 256 * (1 + COOP_GROUPS);
-  const bool table = policy == GSE_POLICY_HEAD_SUM || policy == GSE_POLICY_HEAD_MAX_SUM;
-  L.col32 = o; o += table ? align256(LG * N * 4) : 0;
-  L.bypos = o; o += blk ? align256(LG * n * 4) : 0;
-  L.bscore = o; o += blk ? align256(LG * nblocks * 8) : 0;
-  L.colscore = o; o += blk ? align256(LG * N * 8) : 0;
-  L.slots = o; o += align256(((N + 31) / 32) * 32 * 4);  // whole 32-column words
-  L.keys = o; o += align256(LG * N * 8);
-  L.posw = o; o += align256(LG * N * 4);
-  L.prot = o; o += align256(2 * LG * 4);  // protected counts, then the counts below the tail region
-  L.middle = o; o += align256(LG * budget * 4);
-  L.prot_cols = o; o += align256(budget * 4);
-  L.targets = o; o += align256(budget * 4);
-  L.skv = o; o += align256(LG * budget * 2 * head_dim * 2);
-  L.ssc = o; o += align256(LG * budget * 4);
-  L.total = o;
-  return L;
+  return align256(LG * budget * 2 * head_dim * 2) + align256(LG * budget * 4);
 }
 
 // Grid of the single-pass relocation: every workgroup the device can hold at once (cached per
@@ -1478,14 +1691,330 @@ size_t select_lds_bytes(int nwords) {
   return size_t(128 + 256 + 16) * 4 + size_t(nwords) * 4 + size_t(ngroups) * 4 + 16;
 }
 
+// The selection's keys (and position bitmap) stay in LDS for the whole row.
+bool fits_lds(const BndRow& r) {
+  return r.N <= SEL_LDS_KEYS && 2 * ((r.n + 31) / 32) <= SEL_LDS_KEYS;
+}
+
+int64_t row_candidates(const gse_boundary_row& r) { return r.row_count + r.n - r.row_frontier; }
+
+// Checks what every row of a boundary call must satisfy; returns GSE_OK or the failure.
+int check_boundary(int layers, int kv_heads, int head_dim, int64_t kv_stride_s, int64_t kv_stride_h, int64_t budget,
+                   int policy, int block, int shared, const gse_boundary_row* rows, int n_rows) {
+  if (layers <= 0 || kv_heads <= 0 || budget <= 0 || n_rows < 0)
+    return gse_fail(GSE_EINVAL, "boundary: needs layers, kv_heads, budget > 0");
+  if (head_dim % 8 || head_dim <= 0 || kv_stride_h % 8 || kv_stride_s % 8)
+    return gse_fail(GSE_ESHAPE, "boundary: head_dim and K/V strides must be multiples of 8");
+  if (policy < GSE_POLICY_HEAD_SUM || policy > GSE_POLICY_BLOCK_MAX) return gse_fail(GSE_EINVAL, "boundary: unknown policy");
+  const bool blk = block_policy(policy);
+  if (blk ? (block < 1 || block > 2048) : (block != 1 || shared))
+    return gse_fail(GSE_EINVAL, "boundary: block must be 1..2048 for block policies, 1 (not shared) for others");
+  for (int i = 0; i < n_rows; ++i) {
+    const gse_boundary_row& r = rows[i];
+    const int64_t N = row_candidates(r);
+    if (N <= budget) return gse_fail(GSE_EINVAL, "boundary: every row needs N = row_count + n - row_frontier > budget");
+    if (r.n > MAX_POSITIONS || N >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "boundary: logical length too large");
+    if (r.row_count > 0 && !r.pos_old) return gse_fail(GSE_EINVAL, "boundary: pos_old needed when count > 0");
+    if (policy == GSE_POLICY_RANDOM && !r.random_scores)
+      return gse_fail(GSE_EINVAL, "boundary: random_2048 needs scores");
+    if (!r.pos_new || !r.leftover || !r.status) return gse_fail(GSE_EINVAL, "boundary: null row output");
+    for (int j = 0; j < i; ++j)
+      if (rows[j].row == r.row) return gse_fail(GSE_EINVAL, "boundary: a row appears twice in one batch");
+  }
+  return GSE_OK;
+}
+
+// Block policies: each column's float64 block score, per row (their sizes differ).
+int block_scores(const BndCommon& c, const BndRow& r, hipStream_t s) {
+  const RowLayout L = row_layout(c, r);
+  const int LG = c.layers * c.kv_heads;
+  BlkArgs k = {};
+  k.layers = c.layers;
+  k.kv_heads = c.kv_heads;
+  k.block = c.block;
+  k.shared = c.shared;
+  k.max_mode = c.policy == GSE_POLICY_BLOCK_MAX;
+  k.N = r.N;
+  k.n = r.n;
+  k.nblocks = (r.n + c.block - 1) / c.block;
+  k.count = r.count;
+  k.frontier = r.frontier;
+  k.pos_old = r.pos_old;
+  k.pstride = r.pstride;
+  k.slots = reinterpret_cast<const int32_t*>(r.ws + L.slots);
+  k.scores = c.scores;
+  k.ssl = c.ssl;
+  k.ssg = c.ssg;
+  k.sss = c.sss;
+  k.bypos = reinterpret_cast<float*>(r.ws + L.bypos);
+  k.bscore = reinterpret_cast<double*>(r.ws + L.bscore);
+  k.colscore = reinterpret_cast<double*>(r.ws + L.colscore);
+  hipLaunchKernelGGL(block_clear_kernel, dim3(1024), dim3(256), 0, s, k.bypos, int64_t(LG) * r.n);
+  if (int rc = gse_launch_check("boundary block clear")) return rc;
+  const dim3 cgrid(unsigned((r.N + 255) / 256), unsigned(LG));
+  hipLaunchKernelGGL(block_scatter_kernel, cgrid, dim3(256), 0, s, k);
+  if (int rc = gse_launch_check("boundary block scatter")) return rc;
+  hipLaunchKernelGGL(block_score_kernel, dim3(unsigned((k.nblocks + 255) / 256), unsigned(c.shared ? c.layers : LG)),
+                     dim3(256), 0, s, k);
+  if (int rc = gse_launch_check("boundary block scores")) return rc;
+  hipLaunchKernelGGL(block_column_kernel, cgrid, dim3(256), 0, s, k);
+  return gse_launch_check("boundary block columns");
+}
+
+// One row's relocation: the single pass (with its fallback behind it), else through scratch.
+int relocate_row(const BndCommon& c, const BndRow& r, int coop_blocks, int coop_per, hipStream_t s) {
+  const BndArgs b = bnd_args(c, r);
+  if (coop_blocks > 0) {
+    // An ordinary launch of at most as many workgroups as the device holds at once: the stream's
+    // earlier kernels have retired before it starts, so every workgroup is resident.
+    // (hipLaunchCooperativeKernel guarantees the same but first drains the stream: each launch
+    // then left the GPU idle for about 0.5 ms.)
+    if (coop_per <= 4)
+      hipLaunchKernelGGL(relocate_coop_kernel<4>, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), 0, s, b);
+    else
+      hipLaunchKernelGGL(relocate_coop_kernel<8>, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), 0, s, b);
+    if (int rc = gse_launch_check("boundary relocate")) return rc;
+    // The fallback: if the single pass was abandoned (nothing stored), gather and scatter through
+    // scratch; otherwise these return at once.
+    BndArgs fb = b;
+    fb.fallback_only = 1;
+    const dim3 fgrid(32, unsigned(c.layers));
+    hipLaunchKernelGGL(relocate_rows_kernel<0>, fgrid, dim3(256), 0, s, fb);
+    if (int rc = gse_launch_check("boundary fallback gather")) return rc;
+    hipLaunchKernelGGL(relocate_rows_kernel<1>, fgrid, dim3(256), 0, s, fb);
+    return gse_launch_check("boundary fallback scatter");
+  }
+  if (c.kv_heads == 8 && c.head_dim == 64) {
+    const dim3 rgrid(unsigned((c.budget + 4 * ROWS_PER_WAVE - 1) / (4 * ROWS_PER_WAVE)), unsigned(c.layers));
+    hipLaunchKernelGGL(relocate_rows_kernel<0>, rgrid, dim3(256), 0, s, b);
+    if (int rc = gse_launch_check("boundary gather")) return rc;
+    hipLaunchKernelGGL(relocate_rows_kernel<1>, rgrid, dim3(256), 0, s, b);
+    return gse_launch_check("boundary scatter");
+  }
+  const int chunks = c.head_dim / 8;
+  const dim3 rgrid(unsigned((c.budget * chunks + 255) / 256), unsigned(c.layers * c.kv_heads));
+  hipLaunchKernelGGL(relocate_kernel<0>, rgrid, dim3(256), 0, s, b);
+  if (int rc = gse_launch_check("boundary gather")) return rc;
+  hipLaunchKernelGGL(relocate_kernel<1>, rgrid, dim3(256), 0, s, b);
+  return gse_launch_check("boundary scatter");
+}
+
+// A batch of at most MAX_BATCH rows whose workspace regions are set: one launch per per-row
+// kernel for all rows, then the relocations one row at a time.
+int boundary_launch(const BndCommon& c, const BndRow* rows, int nrows, int coop_blocks, int coop_per, hipStream_t s) {
+  const int LG = c.layers * c.kv_heads;
+  BndBatch b = {};
+  b.c = c;
+  b.nrows = nrows;
+  int64_t max_n_cols = 0, max_words = 0, max_col_words = 0;
+  for (int i = 0; i < nrows; ++i) {
+    b.r[i] = rows[i];
+    max_n_cols = std::max(max_n_cols, rows[i].N);
+    max_words = std::max<int64_t>(max_words, (rows[i].n + 31) / 32);
+    max_col_words = std::max<int64_t>(max_col_words, (rows[i].N + 31) / 32);
+  }
+  const unsigned col_blocks = unsigned((max_n_cols + 255) / 256);
+  hipLaunchKernelGGL(prep_slots_kernel, dim3(col_blocks, unsigned(nrows)), dim3(256), 0, s, b);
+  if (int rc = gse_launch_check("boundary prep")) return rc;
+  if (block_policy(c.policy)) {
+    for (int i = 0; i < nrows; ++i)
+      if (int rc = block_scores(c, rows[i], s)) return rc;
+  } else if (table_policy(c.policy)) {
+    hipLaunchKernelGGL(table_columns_kernel, dim3(col_blocks, unsigned(c.layers), unsigned(nrows)), dim3(256), 0, s,
+                       b);
+    if (int rc = gse_launch_check("boundary table columns")) return rc;
+  }
+  // Selection: rows whose keys fit in LDS in one launch, the others in another.
+  for (int pass = 0; pass < 2; ++pass) {
+    BndBatch sub = {};
+    sub.c = c;
+    int64_t words = 0;
+    for (int i = 0; i < nrows; ++i)
+      if (fits_lds(rows[i]) == (pass == 0)) {
+        sub.r[sub.nrows++] = rows[i];
+        words = std::max<int64_t>(words, (rows[i].n + 31) / 32);
+      }
+    if (!sub.nrows) continue;
+    if (pass == 0)
+      hipLaunchKernelGGL(select_row_kernel, dim3(unsigned(LG + 1), unsigned(sub.nrows)), dim3(SEL_THREADS), 0, s, sub);
+    else
+      hipLaunchKernelGGL(select_kernel<BndBatch>, dim3(unsigned(LG), unsigned(sub.nrows)), dim3(SEL_THREADS),
+                         select_lds_bytes(int(words)), s, sub);
+    if (int rc = gse_launch_check("boundary select")) return rc;
+  }
+  (void)max_words;
+  const size_t col_lds = size_t(128 + 16) * 4 + size_t(max_col_words) * 4 + 16;
+  hipLaunchKernelGGL(columns_kernel, dim3(unsigned(nrows)), dim3(SEL_THREADS), col_lds, s, b);
+  if (int rc = gse_launch_check("boundary columns")) return rc;
+  for (int i = 0; i < nrows; ++i)
+    if (int rc = relocate_row(c, rows[i], coop_blocks, coop_per, s)) return rc;
+  hipLaunchKernelGGL(protected_pos_kernel, dim3(unsigned(LG), unsigned(nrows)), dim3(256), 0, s, b);
+  return gse_launch_check("boundary protected pos");
+}
+
+int boundary_impl(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                  int kv_heads, int head_dim, float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                  int64_t scores_stride_s, int32_t* table, int64_t table_stride, const int32_t* req_to_token,
+                  int64_t r2t_stride, int32_t* frontier, int32_t* count, const gse_boundary_row* rows, int n_rows,
+                  int64_t budget, int64_t prefix, int64_t recent, int policy, int64_t seed, int block, int shared,
+                  void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
+  if (int rc = check_boundary(layers, kv_heads, head_dim, kv_stride_s, kv_stride_h, budget, policy, block, shared,
+                              rows, n_rows))
+    return rc;
+  if (n_rows == 0) return GSE_OK;
+  if (!k_pools || !v_pools || !scores || !table || !req_to_token || !frontier || !count || !workspace || !rows)
+    return gse_fail(GSE_EINVAL, "boundary: null pointer");
+  if (workspace_bytes < gse_boundary_batch_workspace_bytes(layers, kv_heads, head_dim, rows, n_rows, budget, policy,
+                                                           block))
+    return gse_fail(GSE_EWORKSPACE, "boundary: workspace too small");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int64_t LG = int64_t(layers) * kv_heads;
+
+  BndCommon c = {};
+  c.layers = layers;
+  c.kv_heads = kv_heads;
+  c.head_dim = head_dim;
+  c.policy = policy;
+  c.block = block;
+  c.shared = shared ? 1 : 0;
+  c.prefix_sliding = policy == GSE_POLICY_PREFIX_SLIDING;
+  c.budget = budget;
+  c.prefix = prefix;
+  c.recent = recent;
+  c.seed = seed;
+  c.table = table;
+  c.table_stride = table_stride;
+  c.r2t = req_to_token;
+  c.r2t_stride = r2t_stride;
+  c.frontier = frontier;
+  c.count = count;
+  c.k_pools = k_pools;
+  c.v_pools = v_pools;
+  c.kv_ss = kv_stride_s;
+  c.kv_sh = kv_stride_h;
+  c.scores = scores;
+  c.ssl = scores_stride_l;
+  c.ssg = scores_stride_g;
+  c.sss = scores_stride_s;
+  c.scratch_kv = reinterpret_cast<uint16_t*>(ws);
+  c.scratch_sc = reinterpret_cast<float*>(ws + align256(LG * budget * 2 * head_dim * 2));
+  int coop_blocks = 0, coop_per = 0;
+  if (kv_heads == 8 && head_dim == 64 && layers <= COOP_MAX_LAYERS) coop_plan(budget, &coop_blocks, &coop_per);
+  c.relocation = coop_blocks > 0 ? GSE_RELOCATION_SINGLE_PASS : GSE_RELOCATION_SCRATCH;
+  c.coop_spin_limit = COOP_SPIN_LIMIT;
+  c.coop_extra_target = 0;
+  // GSE_RELOCATE_TEST_ABORT=1 (tests only): the first barrier's target is one past the grid, so
+  // its wait can never complete; after 256 polls the single pass is abandoned and the fallback
+  // moves the rows.
+  const char* test_abort = getenv("GSE_RELOCATE_TEST_ABORT");
+  if (test_abort && test_abort[0] == '1') {
+    c.coop_spin_limit = 256;
+    c.coop_extra_target = 1;
+  }
+
+  int64_t offset = scratch_bytes(layers, kv_heads, head_dim, budget);
+  for (int i0 = 0; i0 < n_rows; i0 += MAX_BATCH) {
+    BndRow br[MAX_BATCH];
+    const int nb = std::min(MAX_BATCH, n_rows - i0);
+    for (int k = 0; k < nb; ++k) {
+      const gse_boundary_row& r = rows[i0 + k];
+      BndRow& o = br[k];
+      o = BndRow{};
+      o.row = r.row;
+      o.has_cursor = r.has_cursor ? 1 : 0;
+      o.N = row_candidates(r);
+      o.n = r.n;
+      o.count = r.row_count;
+      o.frontier = r.row_frontier;
+      o.cursor = r.cursor;
+      o.pstride = r.pos_old_stride;
+      o.pos_old = r.pos_old;
+      o.random_scores = r.random_scores;
+      o.pos_new = r.pos_new;
+      o.leftover = r.leftover;
+      o.status = r.status;
+      o.ws = ws + offset;
+      // Block policies place the protected recent region (the blocks of the recent window and of
+      // the sliding-window cursor, [tail_from, n)) after the kept middle, so every row's slot list
+      // ends with its newest positions in order: a score delay is then a cut of the list's last
+      // entries.
+      o.tail_from = r.n;
+      if (block_policy(policy)) {
+        const int64_t edge = std::max<int64_t>(0, std::min(r.n - recent, o.has_cursor ? r.cursor : r.n));
+        o.tail_from = edge - edge % block;
+      }
+      offset += row_layout(c, o).total;
+    }
+    if (int rc = boundary_launch(c, br, nb, coop_blocks, coop_per, s)) return rc;
+  }
+  return GSE_OK;
+}
+
+int live_impl(float* scores, int layers, int64_t scores_stride_l, int kv_heads, int64_t scores_stride_g,
+              int64_t scores_stride_s, const int32_t* table, int64_t table_stride, int32_t* req_to_token,
+              int64_t r2t_stride, const gse_live_row* rows, int n_rows, const void* swa_mapping, int swa_dtype,
+              int64_t num_slots, void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
+  if (!scores || !table || !req_to_token || !workspace || (n_rows > 0 && !rows))
+    return gse_fail(GSE_EINVAL, "boundary_live: null pointer");
+  if (num_slots <= 0 || n_rows < 0) return gse_fail(GSE_EINVAL, "boundary_live: bad sizes");
+  for (int i = 0; i < n_rows; ++i) {
+    if (!rows[i].leftover || !rows[i].status) return gse_fail(GSE_EINVAL, "boundary_live: null row pointer");
+    if (rows[i].true_len < 0 || rows[i].true_len > rows[i].n) return gse_fail(GSE_EINVAL, "boundary_live: bad sizes");
+  }
+  if (workspace_bytes < gse_boundary_live_batch_workspace_bytes(num_slots, n_rows))
+    return gse_fail(GSE_EWORKSPACE, "boundary_live: workspace too small");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t words = gse_boundary_live_workspace_bytes(num_slots);
+  for (int i0 = 0; i0 < n_rows; i0 += MAX_BATCH) {
+    LiveBatch b = {};
+    b.c = LiveCommon{scores, layers, kv_heads, scores_stride_l, scores_stride_g, scores_stride_s, table, table_stride,
+                     req_to_token, r2t_stride, swa_mapping, swa_dtype, num_slots};
+    b.nrows = std::min(MAX_BATCH, n_rows - i0);
+    for (int k = 0; k < b.nrows; ++k) {
+      const gse_live_row& r = rows[i0 + k];
+      b.r[k] = LiveRow{r.row, r.n, r.true_len, r.leftover, r.status,
+                       reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + (i0 + k) * words)};
+    }
+    const unsigned nb = unsigned(b.nrows);
+    // The kernels read each row's leftover count from its status; grid-stride loops cover any count.
+    if (swa_mapping) {
+      hipLaunchKernelGGL(swa_guard_kernel, dim3(64, nb), dim3(256), 0, s, b);
+      if (int rc = gse_launch_check("swa guard")) return rc;
+    }
+    hipLaunchKernelGGL(zero_leftover_kernel, dim3(256, nb), dim3(256), 0, s, b);
+    if (int rc = gse_launch_check("zero leftover")) return rc;
+    if ((num_slots + 31) / 32 <= REPACK_LDS_WORDS)
+      hipLaunchKernelGGL(repack_kernel<true>, dim3(nb), dim3(SEL_THREADS), 0, s, b);
+    else
+      hipLaunchKernelGGL(repack_kernel<false>, dim3(nb), dim3(SEL_THREADS), 0, s, b);
+    if (int rc = gse_launch_check("repack")) return rc;
+  }
+  return GSE_OK;
+}
+
 }  // namespace
+
+extern "C" int64_t gse_boundary_batch_workspace_bytes(int layers, int kv_heads, int head_dim,
+                                                      const gse_boundary_row* rows, int n_rows, int64_t budget,
+                                                      int policy, int block) {
+  int64_t total = scratch_bytes(layers, kv_heads, head_dim, budget);
+  for (int i = 0; i < n_rows; ++i)
+    total += row_layout(layers, kv_heads, row_candidates(rows[i]), rows[i].n, budget, policy, block).total;
+  return total;
+}
 
 extern "C" int64_t gse_boundary_workspace_bytes(int layers, int kv_heads, int head_dim, int64_t n_cols, int64_t n,
                                                 int64_t budget, int policy, int block) {
-  return bnd_layout(layers, kv_heads, head_dim, n_cols, n, budget, policy, block).total;
+  return scratch_bytes(layers, kv_heads, head_dim, budget) +
+         row_layout(layers, kv_heads, n_cols, n, budget, policy, block).total;
 }
 
 extern "C" int64_t gse_boundary_live_workspace_bytes(int64_t num_slots) { return align256(((num_slots + 31) / 32) * 4); }
+
+extern "C" int64_t gse_boundary_live_batch_workspace_bytes(int64_t num_slots, int n_rows) {
+  return gse_boundary_live_workspace_bytes(num_slots) * (n_rows > 0 ? n_rows : 0);
+}
 
 extern "C" int gse_reservoir_scores(const void* pos, int pos_dtype, const int64_t* layer_ids, const int64_t* head_ids,
                                     int layers, int kv_heads, int64_t n, int64_t seed, double* out,
@@ -1529,9 +2058,23 @@ extern "C" int gse_select_kept(const int32_t* pos, const double* score, int laye
   a.prot_count = prot_count;
   a.kept_mask = kept_mask;
   a.nwords = 0;
-  hipLaunchKernelGGL(select_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), select_lds_bytes(0),
+  hipLaunchKernelGGL(select_kernel<SelArgs>, dim3(unsigned(LG)), dim3(SEL_THREADS), select_lds_bytes(0),
                      reinterpret_cast<hipStream_t>(stream), a);
   return gse_launch_check("select");
+}
+
+extern "C" int gse_boundary_batch(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s,
+                                  int64_t kv_stride_h, int kv_heads, int head_dim, float* scores,
+                                  int64_t scores_stride_l, int64_t scores_stride_g, int64_t scores_stride_s,
+                                  int32_t* table, int64_t table_stride, const int32_t* req_to_token,
+                                  int64_t r2t_stride, int32_t* frontier, int32_t* count, const gse_boundary_row* rows,
+                                  int n_rows, int64_t budget, int64_t prefix, int64_t recent, int policy,
+                                  int64_t seed, int block, int shared, void* workspace, int64_t workspace_bytes,
+                                  gse_stream_t stream) {
+  return boundary_impl(k_pools, v_pools, layers, kv_stride_s, kv_stride_h, kv_heads, head_dim, scores,
+                       scores_stride_l, scores_stride_g, scores_stride_s, table, table_stride, req_to_token,
+                       r2t_stride, frontier, count, rows, n_rows, budget, prefix, recent, policy, seed, block, shared,
+                       workspace, workspace_bytes, stream);
 }
 
 extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s,
@@ -1541,221 +2084,25 @@ extern "C" int gse_boundary(void* const* k_pools, void* const* v_pools, int laye
                             int64_t row_count, int64_t row_frontier, const int32_t* pos_old, int64_t pos_old_stride,
                             int64_t n, int64_t budget, int64_t prefix, int64_t recent, int64_t cursor, int has_cursor,
                             int policy, int64_t seed, int block, int shared, const double* random_scores,
-                            int32_t* pos_new,
-                            int64_t* leftover, gse_boundary_status* status, void* workspace, int64_t workspace_bytes,
-                            gse_stream_t stream) {
-  const int64_t N = row_count + n - row_frontier;
-  if (layers <= 0 || kv_heads <= 0 || budget <= 0 || N <= budget)
-    return gse_fail(GSE_EINVAL, "boundary: needs layers, kv_heads, budget > 0 and N > budget");
-  if (head_dim % 8 || head_dim <= 0 || kv_stride_h % 8 || kv_stride_s % 8)
-    return gse_fail(GSE_ESHAPE, "boundary: head_dim and K/V strides must be multiples of 8");
-  if (n > MAX_POSITIONS || N >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "boundary: logical length too large");
-  if (row_count > 0 && !pos_old) return gse_fail(GSE_EINVAL, "boundary: pos_old needed when count > 0");
-  if (policy < GSE_POLICY_HEAD_SUM || policy > GSE_POLICY_BLOCK_MAX) return gse_fail(GSE_EINVAL, "boundary: unknown policy");
-  const bool blk = block_policy(policy);
-  if (blk ? (block < 1 || block > 2048) : (block != 1 || shared))
-    return gse_fail(GSE_EINVAL, "boundary: block must be 1..2048 for block policies, 1 (not shared) for others");
-  if (policy == GSE_POLICY_RANDOM && !random_scores) return gse_fail(GSE_EINVAL, "boundary: random_2048 needs scores");
-  if (!k_pools || !v_pools || !scores || !table || !req_to_token || !frontier || !count || !pos_new || !leftover ||
-      !status)
-    return gse_fail(GSE_EINVAL, "boundary: null pointer");
-  const BndLayout L = bnd_layout(layers, kv_heads, head_dim, N, n, budget, policy, block);
-  if (workspace_bytes < L.total) return gse_fail(GSE_EWORKSPACE, "boundary: workspace too small");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  const int LG = layers * kv_heads;
+                            int32_t* pos_new, int64_t* leftover, gse_boundary_status* status, void* workspace,
+                            int64_t workspace_bytes, gse_stream_t stream) {
+  const gse_boundary_row r = {row, has_cursor, row_count, row_frontier, n, cursor, pos_old, pos_old_stride,
+                              random_scores, pos_new, leftover, status};
+  return boundary_impl(k_pools, v_pools, layers, kv_stride_s, kv_stride_h, kv_heads, head_dim, scores,
+                       scores_stride_l, scores_stride_g, scores_stride_s, table, table_stride, req_to_token,
+                       r2t_stride, frontier, count, &r, 1, budget, prefix, recent, policy, seed, block, shared,
+                       workspace, workspace_bytes, stream);
+}
 
-  BndArgs b = {};
-  b.layers = layers;
-  b.kv_heads = kv_heads;
-  b.head_dim = head_dim;
-  b.N = N;
-  b.n = n;
-  b.budget = budget;
-  b.prefix_sliding = policy == GSE_POLICY_PREFIX_SLIDING;
-  b.block = block;
-  b.table = table;
-  b.table_stride = table_stride;
-  b.r2t = req_to_token;
-  b.r2t_stride = r2t_stride;
-  b.frontier = frontier;
-  b.count = count;
-  b.row = row;
-  b.row_count = row_count;
-  b.row_frontier = row_frontier;
-  b.pos_old = pos_old;
-  b.pstride = pos_old_stride;
-  b.slots = reinterpret_cast<int32_t*>(ws + L.slots);
-  b.prot_count = reinterpret_cast<int32_t*>(ws + L.prot);
-  b.prot_low = b.prot_count + LG;
-  b.middle = reinterpret_cast<int32_t*>(ws + L.middle);
-  b.prot_cols = reinterpret_cast<int32_t*>(ws + L.prot_cols);
-  b.targets = reinterpret_cast<int32_t*>(ws + L.targets);
-  b.pos_new = pos_new;
-  b.leftover = leftover;
-  b.status = status;
-  b.nwords_cols = int((N + 31) / 32);
-  b.k_pools = k_pools;
-  b.v_pools = v_pools;
-  b.kv_ss = kv_stride_s;
-  b.kv_sh = kv_stride_h;
-  b.scores = scores;
-  b.ssl = scores_stride_l;
-  b.ssg = scores_stride_g;
-  b.sss = scores_stride_s;
-  b.scratch_kv = reinterpret_cast<uint16_t*>(ws + L.skv);
-  b.scratch_sc = reinterpret_cast<float*>(ws + L.ssc);
-  b.grid_arrivals = reinterpret_cast<uint32_t*>(ws + L.arrivals);
-
-  hipLaunchKernelGGL(prep_slots_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, s, b);
-  if (int rc = gse_launch_check("boundary prep")) return rc;
-
-  const double* f64_scores = random_scores;
-  if (blk) {
-    BlkArgs k = {};
-    k.layers = layers;
-    k.kv_heads = kv_heads;
-    k.block = block;
-    k.shared = shared ? 1 : 0;
-    k.max_mode = policy == GSE_POLICY_BLOCK_MAX;
-    k.N = N;
-    k.n = n;
-    k.nblocks = (n + block - 1) / block;
-    k.count = row_count;
-    k.frontier = row_frontier;
-    k.pos_old = pos_old;
-    k.pstride = pos_old_stride;
-    k.slots = b.slots;
-    k.scores = scores;
-    k.ssl = scores_stride_l;
-    k.ssg = scores_stride_g;
-    k.sss = scores_stride_s;
-    k.bypos = reinterpret_cast<float*>(ws + L.bypos);
-    k.bscore = reinterpret_cast<double*>(ws + L.bscore);
-    k.colscore = reinterpret_cast<double*>(ws + L.colscore);
-    hipLaunchKernelGGL(block_clear_kernel, dim3(1024), dim3(256), 0, s, k.bypos, int64_t(LG) * n);
-    if (int rc = gse_launch_check("boundary block clear")) return rc;
-    const dim3 cgrid(unsigned((N + 255) / 256), unsigned(LG));
-    hipLaunchKernelGGL(block_scatter_kernel, cgrid, dim3(256), 0, s, k);
-    if (int rc = gse_launch_check("boundary block scatter")) return rc;
-    hipLaunchKernelGGL(block_score_kernel, dim3(unsigned((k.nblocks + 255) / 256), unsigned(shared ? layers : LG)),
-                       dim3(256), 0, s, k);
-    if (int rc = gse_launch_check("boundary block scores")) return rc;
-    hipLaunchKernelGGL(block_column_kernel, cgrid, dim3(256), 0, s, k);
-    if (int rc = gse_launch_check("boundary block columns")) return rc;
-    f64_scores = k.colscore;
-  }
-  float* column_scores = nullptr;
-  if (policy == GSE_POLICY_HEAD_SUM || policy == GSE_POLICY_HEAD_MAX_SUM) {
-    column_scores = reinterpret_cast<float*>(ws + L.col32);
-    hipLaunchKernelGGL(table_columns_kernel, dim3(unsigned((N + 255) / 256), unsigned(layers)), dim3(256), 0, s, scores,
-                       scores_stride_l, scores_stride_g, scores_stride_s, b.slots, kv_heads, N, column_scores);
-    if (int rc = gse_launch_check("boundary table columns")) return rc;
-  }
-
-  SelArgs a = {};
-  a.src.pos_old = pos_old;
-  a.src.pstride = pos_old_stride;
-  a.src.count = row_count;
-  a.src.frontier = row_frontier;
-  a.src.policy = policy;
-  a.src.table_scores = scores;
-  a.src.ssl = scores_stride_l;
-  a.src.ssg = scores_stride_g;
-  a.src.sss = scores_stride_s;
-  a.src.slots = b.slots;
-  a.src.random_scores = f64_scores;
-  a.src.seed = seed;
-  a.src.column_scores = column_scores;
-  a.layers = layers;
-  a.kv_heads = kv_heads;
-  a.n_cols = N;
-  a.n = n;
-  a.budget = budget;
-  a.prefix = prefix;
-  a.recent = recent;
-  a.cursor = cursor;
-  a.has_cursor = has_cursor;
-  a.prefix_sliding = b.prefix_sliding;
-  a.boundary_mode = 1;
-  a.block = block;
-  // Block policies place the protected recent region (the blocks of the recent window and of the
-  // sliding-window cursor, [tail_from, n)) after the kept middle, so every row's slot list ends
-  // with its newest positions in order: a score delay is then a cut of the list's last entries.
-  a.tail_from = n;
-  if (blk) {
-    const int64_t edge = std::max<int64_t>(0, std::min(n - recent, has_cursor ? cursor : n));
-    a.tail_from = edge - edge % block;
-  }
-  a.keys = reinterpret_cast<uint64_t*>(ws + L.keys);
-  a.posw = reinterpret_cast<int32_t*>(ws + L.posw);
-  a.prot_count = b.prot_count;
-  a.prot_low = b.prot_low;
-  a.middle = b.middle;
-  a.prot_cols = b.prot_cols;
-  a.pos_new = pos_new;
-  a.nwords = int((n + 31) / 32);
-  // The position bitmap (and its prefix counts) must fit in the LDS key array of the fast path.
-  // The position bitmap and its per-word prefix must fit in the LDS key array of the fast path.
-  if (N <= SEL_LDS_KEYS && 2 * int64_t(a.nwords) <= SEL_LDS_KEYS)
-    hipLaunchKernelGGL(select_row_kernel, dim3(unsigned(LG + 1)), dim3(SEL_THREADS), 0, s, a);
-  else
-    hipLaunchKernelGGL(select_kernel, dim3(unsigned(LG)), dim3(SEL_THREADS), select_lds_bytes(a.nwords), s, a);
-  if (int rc = gse_launch_check("boundary select")) return rc;
-
-  int coop_blocks = 0, coop_per = 0;
-  if (kv_heads == 8 && head_dim == 64 && layers <= COOP_MAX_LAYERS) coop_plan(budget, &coop_blocks, &coop_per);
-  b.relocation = coop_blocks > 0 ? GSE_RELOCATION_SINGLE_PASS : GSE_RELOCATION_SCRATCH;
-  b.coop_spin_limit = COOP_SPIN_LIMIT;
-  b.coop_extra_target = 0;
-  // GSE_RELOCATE_TEST_ABORT=1 (tests only): the first barrier's target is one past the grid, so
-  // its wait can never complete; after 256 polls the single pass is abandoned and the fallback
-  // moves the rows.
-  const char* test_abort = getenv("GSE_RELOCATE_TEST_ABORT");
-  if (test_abort && test_abort[0] == '1') {
-    b.coop_spin_limit = 256;
-    b.coop_extra_target = 1;
-  }
-
-  const size_t col_lds = size_t(128 + 16) * 4 + size_t(b.nwords_cols) * 4 + 16;
-  hipLaunchKernelGGL(columns_kernel, dim3(1), dim3(SEL_THREADS), col_lds, s, b);
-  if (int rc = gse_launch_check("boundary columns")) return rc;
-
-  if (coop_blocks > 0) {
-    // An ordinary launch of at most as many workgroups as the device holds at once: the stream's
-    // earlier kernels have retired before it starts, so every workgroup is resident.
-    // (hipLaunchCooperativeKernel guarantees the same but first drains the stream: each launch
-    // then left the GPU idle for about 0.5 ms.)
-    if (coop_per <= 4)
-      hipLaunchKernelGGL(relocate_coop_kernel<4>, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), 0, s, b);
-    else
-      hipLaunchKernelGGL(relocate_coop_kernel<8>, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), 0, s, b);
-    if (int rc = gse_launch_check("boundary relocate")) return rc;
-    // The fallback: if the single pass was abandoned (nothing stored), gather and scatter through
-    // scratch; otherwise these return at once.
-    BndArgs fb = b;
-    fb.fallback_only = 1;
-    const dim3 fgrid(32, unsigned(layers));
-    hipLaunchKernelGGL(relocate_rows_kernel<0>, fgrid, dim3(256), 0, s, fb);
-    if (int rc = gse_launch_check("boundary fallback gather")) return rc;
-    hipLaunchKernelGGL(relocate_rows_kernel<1>, fgrid, dim3(256), 0, s, fb);
-    if (int rc = gse_launch_check("boundary fallback scatter")) return rc;
-  } else if (kv_heads == 8 && head_dim == 64) {
-    const dim3 rgrid(unsigned((budget + 4 * ROWS_PER_WAVE - 1) / (4 * ROWS_PER_WAVE)), unsigned(layers));
-    hipLaunchKernelGGL(relocate_rows_kernel<0>, rgrid, dim3(256), 0, s, b);
-    if (int rc = gse_launch_check("boundary gather")) return rc;
-    hipLaunchKernelGGL(relocate_rows_kernel<1>, rgrid, dim3(256), 0, s, b);
-    if (int rc = gse_launch_check("boundary scatter")) return rc;
-  } else {
-    const int chunks = head_dim / 8;
-    const dim3 rgrid(unsigned((budget * chunks + 255) / 256), unsigned(LG));
-    hipLaunchKernelGGL(relocate_kernel<0>, rgrid, dim3(256), 0, s, b);
-    if (int rc = gse_launch_check("boundary gather")) return rc;
-    hipLaunchKernelGGL(relocate_kernel<1>, rgrid, dim3(256), 0, s, b);
-    if (int rc = gse_launch_check("boundary scatter")) return rc;
-  }
-  hipLaunchKernelGGL(protected_pos_kernel, dim3(unsigned(LG)), dim3(256), 0, s, b);
-  return gse_launch_check("boundary protected pos");
+extern "C" int gse_boundary_live_batch(float* scores, int layers, int64_t scores_stride_l, int kv_heads,
+                                       int64_t scores_stride_g, int64_t scores_stride_s, const int32_t* table,
+                                       int64_t table_stride, int32_t* req_to_token, int64_t r2t_stride,
+                                       const gse_live_row* rows, int n_rows, const void* swa_mapping, int swa_dtype,
+                                       int64_t num_slots, void* workspace, int64_t workspace_bytes,
+                                       gse_stream_t stream) {
+  return live_impl(scores, layers, scores_stride_l, kv_heads, scores_stride_g, scores_stride_s, table, table_stride,
+                   req_to_token, r2t_stride, rows, n_rows, swa_mapping, swa_dtype, num_slots, workspace,
+                   workspace_bytes, stream);
 }
 
 extern "C" int gse_boundary_live(float* scores, int layers, int64_t scores_stride_l, int kv_heads,
@@ -1765,25 +2112,8 @@ extern "C" int gse_boundary_live(float* scores, int layers, int64_t scores_strid
                                  const int64_t* leftover, const void* swa_mapping, int swa_dtype, int64_t num_slots,
                                  gse_boundary_status* status, void* workspace, int64_t workspace_bytes,
                                  gse_stream_t stream) {
-  if (!scores || !table || !req_to_token || !leftover || !status || !workspace)
-    return gse_fail(GSE_EINVAL, "boundary_live: null pointer");
-  if (num_slots <= 0 || true_len < 0 || true_len > n) return gse_fail(GSE_EINVAL, "boundary_live: bad sizes");
-  if (workspace_bytes < gse_boundary_live_workspace_bytes(num_slots))
-    return gse_fail(GSE_EWORKSPACE, "boundary_live: workspace too small");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  LiveArgs a = {scores, layers, kv_heads, scores_stride_l, scores_stride_g, scores_stride_s, table, table_stride, req_to_token,
-                r2t_stride, row, n, true_len, leftover, swa_mapping, swa_dtype, num_slots, status,
-                static_cast<uint32_t*>(workspace)};
-  // The kernels read the leftover count from *status; grid-stride loops cover any count.
-  if (swa_mapping) {
-    hipLaunchKernelGGL(swa_guard_kernel, dim3(64), dim3(256), 0, s, a);
-    if (int rc = gse_launch_check("swa guard")) return rc;
-  }
-  hipLaunchKernelGGL(zero_leftover_kernel, dim3(256), dim3(256), 0, s, a);
-  if (int rc = gse_launch_check("zero leftover")) return rc;
-  if ((num_slots + 31) / 32 <= REPACK_LDS_WORDS)
-    hipLaunchKernelGGL(repack_kernel<true>, dim3(1), dim3(SEL_THREADS), 0, s, a);
-  else
-    hipLaunchKernelGGL(repack_kernel<false>, dim3(1), dim3(SEL_THREADS), 0, s, a);
-  return gse_launch_check("repack");
+  const gse_live_row r = {row, n, true_len, leftover, status};
+  return live_impl(scores, layers, scores_stride_l, kv_heads, scores_stride_g, scores_stride_s, table, table_stride,
+                   req_to_token, r2t_stride, &r, 1, swa_mapping, swa_dtype, num_slots, workspace, workspace_bytes,
+                   stream);
 }

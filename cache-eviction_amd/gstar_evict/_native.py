@@ -26,6 +26,19 @@ RELOCATION_SINGLE_PASS, RELOCATION_SCRATCH = 0, 1
 
 _p, _i, _l, _f, _d = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double
 
+
+class BoundaryRow(ctypes.Structure):
+    """gse_boundary_row: one row of gse_boundary_batch (host array, device pointers)."""
+    _fields_ = [("row", ctypes.c_int32), ("has_cursor", ctypes.c_int32), ("row_count", _l), ("row_frontier", _l),
+                ("n", _l), ("cursor", _l), ("pos_old", _p), ("pos_old_stride", _l), ("random_scores", _p),
+                ("pos_new", _p), ("leftover", _p), ("status", _p)]
+
+
+class LiveRow(ctypes.Structure):
+    """gse_live_row: one row of gse_boundary_live_batch."""
+    _fields_ = [("row", ctypes.c_int32), ("n", _l), ("true_len", _l), ("leftover", _p), ("status", _p)]
+
+
 # name -> (restype, argtypes); mirrors include/gstar_evict.h.
 SIGNATURES = {
     "gse_version": (_i, []),
@@ -44,6 +57,11 @@ SIGNATURES = {
     "gse_boundary_workspace_bytes": (_l, [_i, _i, _i, _l, _l, _l, _i, _i]),
     "gse_boundary": (_i, [_p, _p, _i, _l, _l, _i, _i, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _i, _l, _l, _p, _l,
                           _l, _l, _l, _l, _l, _i, _i, _l, _i, _i, _p, _p, _p, _p, _p, _l, _p]),
+    "gse_boundary_batch_workspace_bytes": (_l, [_i, _i, _i, _p, _i, _l, _i, _i]),
+    "gse_boundary_batch": (_i, [_p, _p, _i, _l, _l, _i, _i, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _i, _l, _l,
+                                _l, _i, _l, _i, _i, _p, _l, _p]),
+    "gse_boundary_live_batch_workspace_bytes": (_l, [_l, _i]),
+    "gse_boundary_live_batch": (_i, [_p, _i, _l, _i, _l, _l, _p, _l, _p, _l, _p, _i, _p, _i, _l, _p, _l, _p]),
     "gse_boundary_live_workspace_bytes": (_l, [_l]),
     "gse_boundary_live": (_i, [_p, _i, _l, _i, _l, _l, _p, _l, _p, _l, _i, _l, _l, _p, _p, _i, _l, _p, _p, _l, _p]),
     "gse_prefill_workspace_bytes": (_l, [_l, _i]),

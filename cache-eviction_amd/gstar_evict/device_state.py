@@ -50,7 +50,8 @@ class State:
         self.row_ids = torch.arange(n_rows, **i32)
         self.layer_scaling = {}  # full-layer index -> softmax scale of its queued queries
         self._ws = {}
-        self._status_host = None
+        self._status_blocks = []  # pinned host blocks [rows, 16] of boundary status words
+        self._status_blocks_used = 0
         self._pools = None
         self.pending = []  # boundaries queued on the device whose host part is still to do
         self._rows_host = self._rows_dev = self._rows_copied = None
@@ -68,13 +69,16 @@ class State:
             buf = self._ws[name] = torch.empty(size, dtype=torch.uint8, device=self.device)
         return buf
 
-    def status_host(self, row):
-        """The pinned host copy target of a boundary's status words, one per row (a row has at
-        most one boundary in flight: its next one is a whole interval later and every hook
-        finishes pending boundaries first)."""
-        if self._status_host is None:
-            self._status_host = torch.zeros((self.req_to_token.shape[0], 16), dtype=torch.int32, pin_memory=True)
-        return self._status_host[row]
+    def status_block(self, count=0):
+        """A pinned host block of status rows ([rows, 16] int32, the first ``count`` for one
+        boundary batch): a block of its own for every batch started since the host last finished
+        all pending boundaries, so a block is not written again before its batch is finished."""
+        while self._status_blocks_used >= len(self._status_blocks):
+            self._status_blocks.append(torch.zeros((self.req_to_token.shape[0], 16), dtype=torch.int32,
+                                                   pin_memory=True))
+        block = self._status_blocks[self._status_blocks_used]
+        self._status_blocks_used += 1
+        return block
 
     def row_list(self, rows):
         """``rows`` (host ints) as a device int32 vector, through a persistent pinned buffer: the
@@ -102,6 +106,7 @@ class State:
         from .compaction import finish_boundary
         while self.pending:
             finish_boundary(self, self.pending.pop(0))
+        self._status_blocks_used = 0  # every block's batch is finished
 
     def ensure_queue(self):
         """Allocate the score queues once (the decode kernels fix 8 query heads per KV head)."""
@@ -114,7 +119,8 @@ class State:
         self.qlim = torch.zeros((layers, n_rows, cap), dtype=torch.int32, device=self.device)
         # Pinned host buffers now, at the first decode step: allocating pinned memory
         # synchronises the device, which would drain the GPU if done mid-run.
-        self.status_host(0)
+        self.status_block()
+        self._status_blocks_used = 0
         self._pin_rows()
 
     def pool_pointers(self):

@@ -268,6 +268,46 @@ int gse_boundary(void* const* k_pools, void* const* v_pools, int layers, int64_t
                  const double* random_scores, int32_t* pos_new, int64_t* leftover, gse_boundary_status* status,
                  void* workspace, int64_t workspace_bytes, gse_stream_t stream);
 
+/*
+ * One row of a boundary batch: gse_boundary's per-row arguments. The array is read on the host
+ * during the call; the pointers in it are device memory.
+ */
+typedef struct {
+  int32_t row;                  /* table / req_to_token row (distinct within a batch)            */
+  int32_t has_cursor;           /* 1: `cursor` is the sliding-window guard (R:384-386)           */
+  int64_t row_count;            /* the row's retained columns before the boundary                */
+  int64_t row_frontier;         /* its frontier before the boundary                              */
+  int64_t n;                    /* logical length at the boundary                                */
+  int64_t cursor;
+  const int32_t* pos_old;       /* [L, G, >= row_count] retained positions, rows pos_old_stride
+                                   elements apart; null when row_count is 0                      */
+  int64_t pos_old_stride;
+  const double* random_scores;  /* random_2048: [L, G, N] draws; else null                      */
+  int32_t* pos_new;             /* out: [L, G, budget]                                           */
+  int64_t* leftover;            /* out: N slots (status.leftover of them valid)                  */
+  gse_boundary_status* status;  /* out                                                           */
+} gse_boundary_row;
+
+/* Workspace bytes gse_boundary_batch needs for these rows. */
+int64_t gse_boundary_batch_workspace_bytes(int layers, int kv_heads, int head_dim, const gse_boundary_row* rows,
+                                           int n_rows, int64_t budget, int policy, int block);
+
+/*
+ * boundary_batch — gse_boundary for n_rows rows that share a policy and budget, each row's
+ * result as if it ran alone (R:415-475 per row). No reference counterpart as an entry point: the
+ * reference evicts one request at a time (R:704-710); when several rows reach a boundary at one
+ * decode step (SGLang calls on_decode once per batch), their selections, column splits and
+ * protected positions run as one launch each (up to 8 rows per launch) and their relocations one
+ * row after another. Each row must satisfy gse_boundary's conditions (N > budget).
+ */
+int gse_boundary_batch(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s,
+                       int64_t kv_stride_h, int kv_heads, int head_dim, float* scores, int64_t scores_stride_l,
+                       int64_t scores_stride_g, int64_t scores_stride_s, int32_t* table, int64_t table_stride,
+                       const int32_t* req_to_token, int64_t r2t_stride, int32_t* frontier, int32_t* count,
+                       const gse_boundary_row* rows, int n_rows, int64_t budget, int64_t prefix, int64_t recent,
+                       int policy, int64_t seed, int block, int shared, void* workspace, int64_t workspace_bytes,
+                       gse_stream_t stream);
+
 /* Workspace bytes gse_boundary_live needs for a pool of num_slots slots. */
 int64_t gse_boundary_live_workspace_bytes(int64_t num_slots);
 
@@ -289,6 +329,29 @@ int gse_boundary_live(float* scores, int layers, int64_t scores_stride_l, int kv
                       int row, int64_t n, int64_t true_len, const int64_t* leftover, const void* swa_mapping,
                       int swa_dtype, int64_t num_slots, gse_boundary_status* status, void* workspace,
                       int64_t workspace_bytes, gse_stream_t stream);
+
+/* One row of a live-compaction batch: gse_boundary_live's per-row arguments (host array). */
+typedef struct {
+  int32_t row;
+  int64_t n;
+  int64_t true_len;
+  const int64_t* leftover;       /* the row's gse_boundary leftover output */
+  gse_boundary_status* status;   /* the row's gse_boundary status          */
+} gse_live_row;
+
+/* Workspace bytes gse_boundary_live_batch needs for n_rows rows. */
+int64_t gse_boundary_live_batch_workspace_bytes(int64_t num_slots, int n_rows);
+
+/*
+ * boundary_live_batch — gse_boundary_live for n_rows rows after their gse_boundary_batch (R:476-491
+ * per row); its kernels run once for all rows (up to 8 rows per launch). No reference counterpart
+ * as an entry point, for the same reason as gse_boundary_batch.
+ */
+int gse_boundary_live_batch(float* scores, int layers, int64_t scores_stride_l, int kv_heads,
+                            int64_t scores_stride_g, int64_t scores_stride_s, const int32_t* table,
+                            int64_t table_stride, int32_t* req_to_token, int64_t r2t_stride, const gse_live_row* rows,
+                            int n_rows, const void* swa_mapping, int swa_dtype, int64_t num_slots, void* workspace,
+                            int64_t workspace_bytes, gse_stream_t stream);
 
 /*
  * prefill_scores — one extend chunk's exact per-KV-head column sums, added to

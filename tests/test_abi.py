@@ -79,3 +79,32 @@ def test_score_word_layout_matches_the_header():
     from gstar_evict import requests
     m = re.search(r"#define\s+GSE_SCORE_DELAY_SHIFT\s+(\d+)", open(HEADER).read())
     assert m and int(m.group(1)) == requests.SCORE_DELAY_SHIFT
+
+
+def test_row_descriptors_match_the_header_layout(tmp_path):
+    """The ctypes mirrors of gse_boundary_row and gse_live_row have the C structs' size and
+    field offsets (a C program built against the header reports them)."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    structs = {"gse_boundary_row": _native.BoundaryRow, "gse_live_row": _native.LiveRow}
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "gstar_evict.h"', "int main(void) {"]
+    for cname, mirror in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in mirror._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        name, field, value = line.split()
+        got[(name, field)] = int(value)
+    for cname, mirror in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(mirror), cname
+        for field, _ in mirror._fields_:
+            assert got[(cname, field)] == getattr(mirror, field).offset, (cname, field)
