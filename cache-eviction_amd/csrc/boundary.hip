@@ -237,7 +237,6 @@ struct BndArgs {
   int relocation;           // GSE_RELOCATION_* the host planned (written to the status)
   int coop_spin_limit;      // polls before a barrier wait gives up
   uint32_t coop_extra_target;  // added to the first barrier's target (0; a test sets 1 to force the abort)
-  int fallback_only;        // relocate_rows_kernel: run only if the single pass was abandoned
 };
 
 struct BndCommon {
@@ -294,7 +293,7 @@ GSE_HD RowLayout row_layout(int layers, int kv_heads, int64_t N, int64_t n, int6
   const int64_t nblocks = blk && block > 0 ? (n + block - 1) / block : 0;
   RowLayout L;
   int64_t o = 0;
-  L.arrivals = o; o += 256 * (1 + COOP_GROUPS);
+  L.arrivals = o; o += 256 * (2 + COOP_GROUPS);  // barrier counters, then the fallback's done count
   L.col32 = o; o += table_policy(policy) ? align256(LG * N * 4) : 0;
   L.bypos = o; o += blk ? align256(LG * n * 4) : 0;
   L.bscore = o; o += blk ? align256(LG * nblocks * 8) : 0;
@@ -363,7 +362,6 @@ GSE_HD BndArgs bnd_args(const BndCommon& c, const BndRow& r) {
   a.relocation = c.relocation;
   a.coop_spin_limit = c.coop_spin_limit;
   a.coop_extra_target = c.coop_extra_target;
-  a.fallback_only = 0;
   return a;
 }
 
@@ -983,7 +981,7 @@ __global__ void prep_slots_kernel(BndBatch b) {
   const BndArgs a = bnd_args(b.c, b.r[blockIdx.y]);
   const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (c == 0 && a.grid_arrivals)
-    for (int k = 0; k <= COOP_GROUPS; ++k) a.grid_arrivals[64 * k] = 0;  // the top and group counters
+    for (int k = 0; k <= COOP_GROUPS + 1; ++k) a.grid_arrivals[64 * k] = 0;  // top, group and done counters
   if (c >= a.N) return;
   a.slots[c] = c < a.row_count ? a.table[int64_t(a.row) * a.table_stride + c]
                                : a.r2t[int64_t(a.row) * a.r2t_stride + a.row_frontier + c - a.row_count];
@@ -1147,12 +1145,6 @@ template <int DIR>
 __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
   const gse_boundary_status st = *a.status;
   if (st.state != GSE_BOUNDARY_EVICTED || st.width <= 0) return;
-  if (a.fallback_only) {
-    // Behind the single pass: move the rows only if it was abandoned before any store.
-    if (!(__hip_atomic_load(a.grid_arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & COOP_ABORT)) return;
-    if (DIR == 0 && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
-      a.status->relocation = GSE_RELOCATION_SCRATCH;
-  }
   const int64_t width = st.width;
   const int l = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1166,7 +1158,7 @@ __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
   auto sk = [&](int64_t j) { return a.scratch_kv + ((int64_t(l) * a.budget + j) * 2) * (8 * 64) + 64 * g + 8 * piece; };
   auto ss = [&](int64_t j) { return a.scratch_sc + (int64_t(l) * a.budget + j) * 8 + g; };
   // Blocks of 4 * ROWS_PER_WAVE entries, strided over the grid (one block each when the grid
-  // covers the budget; the fallback launch uses a small grid).
+  // covers the budget).
   for (int64_t jb = blockIdx.x; jb * 4 * ROWS_PER_WAVE < width; jb += gridDim.x) {
   const int64_t j0 = (jb * 4 + wave) * ROWS_PER_WAVE;
   if (DIR == 0) {
@@ -1226,8 +1218,8 @@ __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
 // pool is written in exactly one phase, so loads of a later phase never meet a store of an
 // earlier one). A barrier's wait is bounded: past 2^18 polls (about 0.3 s) a workgroup stops
 // waiting. In the first phase nothing has been stored: the waiting workgroup abandons the single
-// pass (COOP_ABORT), every workgroup returns without a store, and relocate_rows_kernel, launched
-// behind it in fallback mode, moves the rows through scratch. Once every workgroup has arrived at
+// pass (COOP_ABORT), no workgroup stores anything of it, and the rows move through scratch
+// instead (coop_fallback). Once every workgroup has arrived at
 // the first barrier all of them are resident, so a later wait cannot outlast the limit in
 // practice; if one did, it marks the boundary GSE_BOUNDARY_ERR_RELOCATE, which the host raises.
 
@@ -1296,6 +1288,58 @@ GSE_DEVICE bool grid_wait(BndArgs& a, uint32_t phase, bool& gave_up, uint32_t* g
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   return phase != 0 || *go != 0;
+}
+
+// The single pass's relocation through scratch, after its first barrier was abandoned (nothing
+// stored, see grid_wait): every workgroup gathers its own waves' entries of every layer into
+// scratch and counts itself done; the last one to do so then scatters every entry from scratch
+// to its target. Its workgroups need not be resident together (those that start later find the
+// abort at once), so this always completes, on one workgroup's bandwidth for the scatter: a path
+// for a device that could not hold the whole grid, not a fast one.
+GSE_DEVICE void coop_fallback(const BndArgs& a, uint16_t* const (*pools)[COOP_MAX_LAYERS], int64_t width,
+                              int64_t j0, int64_t jend, uint32_t* last_flag) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 3, piece = lane & 7;
+  const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
+  // Scratch entry (l, j): K row (8 heads x 64) then V row, bf16; score row (8 heads).
+  auto sk = [&](int l, int64_t j) {
+    return a.scratch_kv + ((int64_t(l) * a.budget + j) * 2) * (8 * 64) + 64 * g + 8 * piece;
+  };
+  auto ss = [&](int l, int64_t j) { return a.scratch_sc + (int64_t(l) * a.budget + j) * 8 + g; };
+  for (int l = 0; l < a.layers; ++l) {
+    auto K = as_global(static_cast<const uint16_t*>(pools[0][l]));
+    auto V = as_global(static_cast<const uint16_t*>(pools[1][l]));
+    const float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
+    const int32_t* m = a.middle + int64_t(l * a.kv_heads + g) * a.budget;
+    for (int64_t j = j0; j < jend; ++j) {
+      const int64_t src = a.slots[m[j]];
+      *reinterpret_cast<uint4*>(sk(l, j)) = gload16(K + src * a.kv_ss + off);
+      *reinterpret_cast<uint4*>(sk(l, j) + 8 * 64) = gload16(V + src * a.kv_ss + off);
+      if (piece == 0) *ss(l, j) = srow[src * a.sss];
+    }
+  }
+  __threadfence();  // this workgroup's scratch rows are visible device-wide before it counts
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t before = atomicAdd(a.grid_arrivals + 64 * (COOP_GROUPS + 1), 1u);
+    *last_flag = before + 1 == gridDim.x;
+  }
+  __syncthreads();
+  if (!*last_flag) return;
+  __threadfence();
+  const int wave = threadIdx.x >> 6;
+  for (int l = 0; l < a.layers; ++l) {
+    auto K = as_global(pools[0][l]);
+    auto V = as_global(pools[1][l]);
+    float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
+    for (int64_t j = wave; j < width; j += COOP_WAVES) {
+      const int64_t dst = a.targets[j];
+      gstore16(K + dst * a.kv_ss + off, *reinterpret_cast<const uint4*>(sk(l, j)));
+      gstore16(V + dst * a.kv_ss + off, *reinterpret_cast<const uint4*>(sk(l, j) + 8 * 64));
+      if (piece == 0) srow[dst * a.sss] = *ss(l, j);
+    }
+  }
+  if (threadIdx.x == 0) a.status->relocation = GSE_RELOCATION_SCRATCH;
 }
 
 template <int PER>
@@ -1367,7 +1411,10 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
     grid_arrive(a, uint32_t(2 * l));
     load_v(l);
     if (l + 1 < a.layers) sources(l + 1);  // the V loads have taken their addresses
-    if (!grid_wait(a, uint32_t(2 * l), gave_up, &go)) return;  // abandoned: nothing stored
+    if (!grid_wait(a, uint32_t(2 * l), gave_up, &go)) {  // abandoned before any store
+      coop_fallback(a, pools, width, j0, last + 1, &go);  // [j0, min(j0 + per, width)): empty past the width
+      return;
+    }
     {
       auto K = as_global(pools[0][l]);
       float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
@@ -1773,16 +1820,7 @@ int relocate_row(const BndCommon& c, const BndRow& r, int coop_blocks, int coop_
       hipLaunchKernelGGL(relocate_coop_kernel<4>, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), 0, s, b);
     else
       hipLaunchKernelGGL(relocate_coop_kernel<8>, dim3(unsigned(coop_blocks)), dim3(COOP_THREADS), 0, s, b);
-    if (int rc = gse_launch_check("boundary relocate")) return rc;
-    // The fallback: if the single pass was abandoned (nothing stored), gather and scatter through
-    // scratch; otherwise these return at once.
-    BndArgs fb = b;
-    fb.fallback_only = 1;
-    const dim3 fgrid(32, unsigned(c.layers));
-    hipLaunchKernelGGL(relocate_rows_kernel<0>, fgrid, dim3(256), 0, s, fb);
-    if (int rc = gse_launch_check("boundary fallback gather")) return rc;
-    hipLaunchKernelGGL(relocate_rows_kernel<1>, fgrid, dim3(256), 0, s, fb);
-    return gse_launch_check("boundary fallback scatter");
+    return gse_launch_check("boundary relocate");
   }
   if (c.kv_heads == 8 && c.head_dim == 64) {
     const dim3 rgrid(unsigned((c.budget + 4 * ROWS_PER_WAVE - 1) / (4 * ROWS_PER_WAVE)), unsigned(c.layers));
