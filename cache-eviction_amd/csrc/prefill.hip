@@ -146,6 +146,16 @@ GSE_DEVICE void prefill_tile(const bf16x8_t (&qa)[RB][2], const bf16x8_t (&kb0)[
           cs[kb] += (p0 + p1) + (p2 + p3);
       }
     }
+    // Alternate the next row-block's 8 MFMAs with this one's vector work (1 MFMA, then 6 vector
+    // instructions): a SIMD overlaps an MFMA only with the independent vector instructions its
+    // own wave issues behind it (the waves' MFMA and vector work do not overlap each other).
+    if (rb + 1 < RB) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six vector ALU instructions
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
 }
