@@ -13,10 +13,25 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 // Wavefront size on CDNA is 64.
 constexpr int kWave = 64;
 
-// A score word (a row's mode_by_row entry, a prefill call's mode): the score mode in bits 0-7
-// (1 sum, 2 max over a KV head's query heads) and the score delay above it, in list entries.
-GSE_DEVICE int score_kind(int32_t word) { return word & 0xff; }
+// A score word (a row's mode_by_row entry, a prefill call's mode): the score kind in bits 0-3
+// (1 sum, 2 max over a KV head's query heads, 4 block counters), log2 of the block size in
+// bits 4-7 (kind 4) and the score delay from bit 8, in list entries.
+// Blocks of kind 4 hold at most 64 entries (one wave's lanes); a larger shift scores nothing.
+GSE_DEVICE int score_block_shift(int32_t word) { return (word >> 4) & 0xf; }
+GSE_DEVICE int score_kind(int32_t word) {
+  const int kind = word & 0xf;
+  return kind == GSE_SCORE_KIND_BLOCK_STEP && score_block_shift(word) > 6 ? 0 : kind;
+}
 GSE_DEVICE int score_delay(int32_t word) { return word >> GSE_SCORE_DELAY_SHIFT; }
+// Kinds that add scores (the others are attention only).
+GSE_DEVICE bool scoring_kind(int kind) { return kind == 1 || kind == 2 || kind == GSE_SCORE_KIND_BLOCK_STEP; }
+// Kind 4: of a list of `lim` entries (the query's own key last), the entries whose blocks a
+// query credits: whole blocks of 2^shift aligned entries whose newest entry is at least
+// `delay` entries older than the query.
+GSE_DEVICE int block_step_limit(int lim, int delay, int shift) {
+  const int n = lim - delay;
+  return n > 0 ? (n >> shift) << shift : 0;
+}
 
 GSE_DEVICE float bf16_to_f32(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
 

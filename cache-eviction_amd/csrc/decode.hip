@@ -319,7 +319,7 @@ __global__ __launch_bounds__(MERGE_THREADS * SPLIT) void decode_merge_kernel(Mer
     row = load_index_dyn(a.rows, a.rows_dtype, b);
     const int md = score_kind(a.mode[row]);
     slot = a.qcount[row] & QUEUE_COUNT_MASK;
-    queue = md == 1 || md == 2;
+    queue = scoring_kind(md);
   }
   const bool live = h < a.q_heads;
   const int hh = live ? h : 0;
@@ -423,28 +423,66 @@ struct ScoreArgs {
   float scale2;
 };
 
+constexpr int SCORE_MAX_CHUNK = 1024;  // keys per workgroup of decode_score_kernel
+
+// Kind 4's fold of kmax[g][key - k0] (keys [k0, k_end), k_end - k0 a multiple of the block):
+// thread t takes keys k0 + t + 512 i; a 64-lane wave covers 64 aligned entries, so a block's
+// maximum is a butterfly over the low `shift` lane bits.
+template <typename IdxT>
+GSE_DEVICE void block_step_reduce(const ScoreArgs& a, const float (*kmax)[SCORE_MAX_CHUNK], const IdxT* idx, int k0,
+                                  int k_end, int shift) {
+  const int lane = threadIdx.x & 63;
+  for (int base = 0; base < k_end - k0; base += blockDim.x) {
+    const int key = base + int(threadIdx.x);
+    // k_end - k0 is a multiple of the block, so a block's lanes are all live or all idle.
+    const bool live = key < k_end - k0;
+    float m = 0.f;
+    if (live)
+      for (int g = 0; g < a.kv_heads; ++g) m = fmaxf(m, kmax[g][key]);
+    for (int o = 1; o < (1 << shift); o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+    if (live && (lane & ((1 << shift) - 1)) == 0) {
+      const int32_t s = int32_t(idx[k0 + key]);
+      a.scores[uint64_t(uint32_t(s)) * a.scores_ss] += m;
+    }
+  }
+}
+
 // Grid (splits, bs), 512 threads: wave g = KV head g over keys [split*chunk, +chunk) of
 // sequence b (the list's first len - delay entries). Per 16 keys, Sp = Q . K^T ([16 heads x
 // 16 keys], heads 8-15 padding), so a lane holds 4 heads of one key: sum / max over heads is
 // in-lane plus one lane swap.
+// Kind 4 (block counters): each wave leaves its keys' maxima over its query heads in LDS; then
+// per key the maximum over the KV heads and per block the maximum over its keys (lane swaps:
+// blocks of at most 64 entries are aligned lane groups of a wave), added to KV head 0's score
+// of the block's first slot. chunk is a multiple of 64, so no block spans two workgroups.
 template <typename IdxT>
 __global__ __launch_bounds__(512) void decode_score_kernel(ScoreArgs a) {
+  __shared__ float kmax[MAX_KVH][SCORE_MAX_CHUNK];
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int g = threadIdx.x >> 6;
-  if (g >= a.kv_heads) return;
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int64_t row = load_index_dyn(a.rows, a.rows_dtype, b);
   const int word = a.mode[row];
   const int md = score_kind(word);
-  if (md != 1 && md != 2) return;
-  const bool max_mode = md == 2;
+  if (!scoring_kind(md)) return;
+  const bool blocks = md == GSE_SCORE_KIND_BLOCK_STEP;
+  if (g >= a.kv_heads && !blocks) return;
+  const bool max_mode = md != 1;
   const int base = a.indptr[b];
-  const int len = a.indptr[b + 1] - base - score_delay(word);  // keys the query scores
+  const int full = a.indptr[b + 1] - base;
+  const int len = blocks ? block_step_limit(full, score_delay(word), score_block_shift(word))
+                         : full - score_delay(word);  // keys the query scores
   const int k0 = blockIdx.x * a.chunk;
   const int k_end = k0 + a.chunk < len ? k0 + a.chunk : len;
   if (k0 >= k_end) return;
+  const IdxT* idx = static_cast<const IdxT*>(a.indices) + base;
+  if (blocks && g >= a.kv_heads) {  // idle wave: only the reduction below
+    __syncthreads();
+    block_step_reduce(a, kmax, idx, k0, k_end, score_block_shift(word));
+    return;
+  }
 
   // A rows: heads g*8 + col (zero for col >= 8), dims [8*grp, +8) and [32 + 8*grp, +8).
   bf16x8_t qa0 = {}, qa1 = {};
@@ -459,7 +497,6 @@ __global__ __launch_bounds__(512) void decode_score_kernel(ScoreArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) nrm[r] = a.norm[int64_t(b) * a.q_heads + g * GROUP + 4 * grp + r] * kLog2e;
 
-  const IdxT* idx = static_cast<const IdxT*>(a.indices) + base;
   const uint16_t* kbase = a.k + int64_t(g) * a.kv_sh + 8 * grp;
   float* srow = a.scores + int64_t(g) * a.scores_sg;
   for (int tb = k0; tb < k_end; tb += 16) {
@@ -475,7 +512,15 @@ __global__ __launch_bounds__(512) void decode_score_kernel(ScoreArgs a) {
     const float u3 = fast_exp2(fmaf(d[3], a.scale2, -nrm[3]));
     // Heads 0-3 (group 0) with heads 4-7 (group 1); groups 2, 3 carry padding (exactly 0).
     const float tot = max_mode ? xor16_max(fmaxf(fmaxf(u0, u1), fmaxf(u2, u3))) : xor16_sum((u0 + u1) + (u2 + u3));
-    if (grp == 0 && key < k_end) srow[uint64_t(uint32_t(s)) * a.scores_ss] += tot;
+    if (blocks) {
+      if (grp == 0 && key < k_end) kmax[g][key - k0] = tot;
+    } else if (grp == 0 && key < k_end) {
+      srow[uint64_t(uint32_t(s)) * a.scores_ss] += tot;
+    }
+  }
+  if (blocks) {
+    __syncthreads();
+    block_step_reduce(a, kmax, idx, k0, k_end, score_block_shift(word));
   }
 }
 

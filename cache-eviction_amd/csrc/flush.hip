@@ -211,6 +211,115 @@ __global__ __launch_bounds__(fl::THREADS) void score_flush_kernel(FlushArgs a) {
   }
 }
 
+// Kind 4 (block counters; TEX:197, no reference code). A workgroup owns (layer, row, 128 keys)
+// for every KV head: wave g keeps K_g of the 128 keys in registers and runs, per pair of queued
+// queries, D = [Q_i; Q_i+1] . K_g^T (the query rows of g's heads, read from the queue), so a lane
+// ends with the maximum over g's heads of one (query, key) after one lane swap; the lanes fold it
+// into qk[query][key] in LDS with an unsigned max (probabilities are non-negative, so their bit
+// patterns order as the values do). Then the threads of the first 128 keys take, per queued query
+// in queue order, the block's maximum over its keys (a butterfly over the low lanes: blocks of at
+// most 64 aligned entries sit in one wave) and the block's first key adds it to its counter,
+// KV head 0's score of its slot, step by step as the per-step update would.
+namespace flb {
+constexpr int WAVES = 8;  // wave g = KV head g
+constexpr int THREADS = WAVES * 64;
+constexpr int KEYS = 128;  // keys per workgroup
+constexpr int SUB = KEYS / 16;
+}  // namespace flb
+
+// Grid (key chunks of 128, n_rows, layers), flb::THREADS threads.
+__global__ __launch_bounds__(flb::THREADS) void score_flush_block_kernel(FlushArgs a) {
+  using namespace flb;
+  __shared__ uint32_t qk[fl::MAX_QUEUE][KEYS];
+  __shared__ int lims[fl::MAX_QUEUE + 1];
+
+  const int l = blockIdx.z;
+  const int64_t row = load_index_dyn(a.rows, a.rows_dtype, blockIdx.y);
+  const int word = a.mode[row];
+  if (score_kind(word) != GSE_SCORE_KIND_BLOCK_STEP) return;
+  const int shift = score_block_shift(word);
+  const int64_t qbase = int64_t(l) * a.rows_total + row;  // (layer, row) queue index
+  int m = a.pcount[qbase];
+  m = m < a.cap ? m : a.cap;
+  if (m <= 0) return;
+  // Credited entries of each queued query: whole blocks at least `delay` entries old.
+  if (threadIdx.x < m)
+    lims[threadIdx.x] = block_step_limit(a.plim[qbase * a.cap + threadIdx.x], score_delay(word), shift);
+  if (threadIdx.x == m) lims[m] = 0;  // the missing query of an odd last pair credits nothing
+  for (int t = threadIdx.x; t < m * KEYS; t += blockDim.x) qk[t / KEYS][t % KEYS] = 0u;
+  __syncthreads();
+  int maxlim = 0;
+  for (int i = 0; i < m; ++i) maxlim = lims[i] > maxlim ? lims[i] : maxlim;
+  const int c0 = blockIdx.x * KEYS;
+  if (c0 >= maxlim) return;
+
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t cnt = a.count[row], fr = a.frontier[row];
+  auto slot_of = [&](int c) -> int32_t {
+    const int cc = c < maxlim ? c : maxlim - 1;
+    const int32_t s = cc < cnt ? a.table[row * a.table_stride + cc] : a.r2t[row * a.r2t_stride + fr + cc - cnt];
+    return c < maxlim ? s : 0;
+  };
+  if (g < a.kv_heads) {
+    const auto kp = as_global(static_cast<const uint16_t*>(a.k_pools[l])) + int64_t(g) * a.kv_sh + 8 * grp;
+    uint4 kf[SUB][2];
+#pragma unroll
+    for (int st = 0; st < SUB; ++st) {
+      const auto p = kp + uint64_t(uint32_t(slot_of(c0 + 16 * st + col))) * uint64_t(a.kv_ss);
+      kf[st][0] = gload16(p);
+      kf[st][1] = gload16(p + 32);
+    }
+    const int npairs = (m + 1) >> 1;
+    for (int pr = 0; pr < npairs; ++pr) {
+      const int la = lims[2 * pr], lb = lims[2 * pr + 1];
+      if (__builtin_amdgcn_readfirstlane(la > lb ? la : lb) <= c0) continue;  // both credit nothing here
+      // A rows: (query 2*pr + col/8, head g*8 + col%8); this lane's D rows: query 2*pr + grp/2,
+      // heads g*8 + 4*(grp%2) + r.
+      const int qa = 2 * pr + (col >> 3);
+      bf16x8_t qa0 = {}, qa1 = {};
+      if (qa < m) {
+        const uint16_t* qp = a.pq + ((qbase * a.cap + qa) * a.q_heads + g * fl::GROUP + (col & 7)) * fl::D + 8 * grp;
+        qa0 = as_bf16x8(*reinterpret_cast<const uint4*>(qp));
+        qa1 = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 32));
+      }
+      const int qd = 2 * pr + (grp >> 1);
+      f32x4_t nrm = {INFINITY, INFINITY, INFINITY, INFINITY};
+      if (qd < m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          nrm[r] = a.pnorm[(qbase * a.cap + qd) * a.q_heads + g * fl::GROUP + 4 * (grp & 1) + r] * kLog2e;
+      const int lim = lims[qd];
+#pragma unroll
+      for (int st = 0; st < SUB; ++st) {
+        f32x4_t d = mfma16x16x32(qa0, as_bf16x8(kf[st][0]), f32x4_t{0.f, 0.f, 0.f, 0.f});
+        d = mfma16x16x32(qa1, as_bf16x8(kf[st][1]), d);
+        const float e0 = fast_exp2(fmaf(d[0], a.scale2, -nrm[0]));
+        const float e1 = fast_exp2(fmaf(d[1], a.scale2, -nrm[1]));
+        const float e2 = fast_exp2(fmaf(d[2], a.scale2, -nrm[2]));
+        const float e3 = fast_exp2(fmaf(d[3], a.scale2, -nrm[3]));
+        const float mx = xor16_max(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
+        const int c = c0 + 16 * st + col;
+        if ((grp & 1) == 0 && c < lim) atomicMax(&qk[qd][16 * st + col], __float_as_uint(mx));
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < KEYS) {
+    const int t = threadIdx.x;
+    const int c = c0 + t;
+    const bool first = (t & ((1 << shift) - 1)) == 0 && c < maxlim;
+    float* cell = first ? a.scores + int64_t(l) * a.ssl + uint64_t(uint32_t(slot_of(c))) * a.sss : nullptr;
+    float counter = first ? *cell : 0.f;
+    for (int q = 0; q < m; ++q) {
+      float v = __uint_as_float(qk[q][t]);
+      for (int o = 1; o < (1 << shift); o <<= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+      counter += v;
+    }
+    if (first) *cell = counter;
+  }
+}
+
 // The queues of the flushed (layer, row) pairs are empty afterwards; a count above the
 // capacity (steps the decode merge could not queue) sets *overflow.
 __global__ void flush_clear_kernel(const void* rows, int rows_dtype, int n_rows, int layers, int rows_total, int cap,
@@ -227,15 +336,15 @@ __global__ void flush_clear_kernel(const void* rows, int rows_dtype, int n_rows,
 
 using namespace gse;
 
-extern "C" int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
-                               float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
-                               int64_t scores_stride_s, const int32_t* table, int64_t table_stride,
-                               const int32_t* req_to_token, int64_t r2t_stride, const int32_t* frontier,
-                               const int32_t* count, const int32_t* mode_by_row, const void* rows, int rows_dtype,
-                               int n_rows, int64_t max_len, const void* pend_q, const float* pend_norm,
-                               const int32_t* pend_lim, int32_t* pend_count, int rows_total, int queue_cap,
-                               int q_heads, int kv_heads, int head_dim, float sm_scale, int32_t* overflow,
-                               gse_stream_t stream) {
+namespace {
+
+// Checks and kernel arguments shared by the two flush entry points; returns GSE_OK or an error.
+int flush_args(FlushArgs& f, void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h, float* scores,
+               int64_t ssl, int64_t ssg, int64_t sss, const int32_t* table, int64_t table_stride,
+               const int32_t* req_to_token, int64_t r2t_stride, const int32_t* frontier, const int32_t* count,
+               const int32_t* mode_by_row, const void* rows, int rows_dtype, int n_rows, int64_t max_len,
+               const void* pend_q, const float* pend_norm, const int32_t* pend_lim, int32_t* pend_count,
+               int rows_total, int queue_cap, int q_heads, int kv_heads, int head_dim, float sm_scale) {
   using namespace fl;
   if (head_dim != D || kv_heads < 1 || kv_heads > 8 || q_heads != GROUP * kv_heads)
     return gse_fail(GSE_ESHAPE, "score_flush: need head_dim 64 and q_heads == 8 * kv_heads <= 64");
@@ -247,19 +356,71 @@ extern "C" int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stri
       !pend_norm || !pend_lim || !pend_count)
     return gse_fail(GSE_EINVAL, "score_flush: null pointer");
   if (max_len >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "score_flush: max_len too large");
+  f = FlushArgs{k_pools, kv_stride_s, kv_stride_h, scores, ssl, ssg, sss, table, table_stride, req_to_token,
+                r2t_stride, frontier, count, mode_by_row, rows, rows_dtype, static_cast<const uint16_t*>(pend_q),
+                pend_norm, pend_lim, pend_count, rows_total, queue_cap, layers, q_heads, kv_heads,
+                sm_scale * kLog2e};
+  return GSE_OK;
+}
+
+int flush_clear(const FlushArgs& f, int n_rows, int32_t* overflow, hipStream_t s) {
+  const int total = n_rows * f.layers;
+  hipLaunchKernelGGL(flush_clear_kernel, dim3((total + 255) / 256), dim3(256), 0, s, f.rows, f.rows_dtype, n_rows,
+                     f.layers, f.rows_total, f.cap, f.pcount, overflow);
+  return gse_launch_check("score_flush clear");
+}
+
+}  // namespace
+
+extern "C" int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                               float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                               int64_t scores_stride_s, const int32_t* table, int64_t table_stride,
+                               const int32_t* req_to_token, int64_t r2t_stride, const int32_t* frontier,
+                               const int32_t* count, const int32_t* mode_by_row, const void* rows, int rows_dtype,
+                               int n_rows, int64_t max_len, const void* pend_q, const float* pend_norm,
+                               const int32_t* pend_lim, int32_t* pend_count, int rows_total, int queue_cap,
+                               int q_heads, int kv_heads, int head_dim, float sm_scale, int32_t* overflow,
+                               gse_stream_t stream) {
+  using namespace fl;
+  FlushArgs f = {};
+  if (int rc = flush_args(f, k_pools, layers, kv_stride_s, kv_stride_h, scores, scores_stride_l, scores_stride_g,
+                          scores_stride_s, table, table_stride, req_to_token, r2t_stride, frontier, count,
+                          mode_by_row, rows, rows_dtype, n_rows, max_len, pend_q, pend_norm, pend_lim, pend_count,
+                          rows_total, queue_cap, q_heads, kv_heads, head_dim, sm_scale))
+    return rc;
+  if (n_rows == 0 || layers == 0) return GSE_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  FlushArgs f = {k_pools, kv_stride_s, kv_stride_h, scores, scores_stride_l, scores_stride_g, scores_stride_s,
-                 table, table_stride, req_to_token, r2t_stride, frontier, count, mode_by_row, rows, rows_dtype,
-                 static_cast<const uint16_t*>(pend_q), pend_norm, pend_lim, pend_count, rows_total, queue_cap,
-                 layers, q_heads, kv_heads, sm_scale * kLog2e};
   const unsigned chunks = unsigned((max_len + CHUNK - 1) / CHUNK);
   if (chunks) {
     hipLaunchKernelGGL(score_flush_kernel, dim3(chunks, unsigned(n_rows), unsigned(layers * kv_heads)), dim3(THREADS),
                        0, s, f);
     if (int rc = gse_launch_check("score_flush")) return rc;
   }
-  const int total = n_rows * layers;
-  hipLaunchKernelGGL(flush_clear_kernel, dim3((total + 255) / 256), dim3(256), 0, s, rows, rows_dtype, n_rows, layers,
-                     rows_total, queue_cap, pend_count, overflow);
-  return gse_launch_check("score_flush clear");
+  return flush_clear(f, n_rows, overflow, s);
+}
+
+extern "C" int gse_score_flush_blocks(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                                      float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                                      int64_t scores_stride_s, const int32_t* table, int64_t table_stride,
+                                      const int32_t* req_to_token, int64_t r2t_stride, const int32_t* frontier,
+                                      const int32_t* count, const int32_t* mode_by_row, const void* rows,
+                                      int rows_dtype, int n_rows, int64_t max_len, const void* pend_q,
+                                      const float* pend_norm, const int32_t* pend_lim, int32_t* pend_count,
+                                      int rows_total, int queue_cap, int q_heads, int kv_heads, int head_dim,
+                                      float sm_scale, int32_t* overflow, gse_stream_t stream) {
+  FlushArgs f = {};
+  if (int rc = flush_args(f, k_pools, layers, kv_stride_s, kv_stride_h, scores, scores_stride_l, scores_stride_g,
+                          scores_stride_s, table, table_stride, req_to_token, r2t_stride, frontier, count,
+                          mode_by_row, rows, rows_dtype, n_rows, max_len, pend_q, pend_norm, pend_lim, pend_count,
+                          rows_total, queue_cap, q_heads, kv_heads, head_dim, sm_scale))
+    return rc;
+  if (n_rows == 0 || layers == 0) return GSE_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const unsigned chunks = unsigned((max_len + flb::KEYS - 1) / flb::KEYS);
+  if (chunks) {
+    hipLaunchKernelGGL(score_flush_block_kernel, dim3(chunks, unsigned(n_rows), unsigned(layers)), dim3(flb::THREADS),
+                       0, s, f);
+    if (int rc = gse_launch_check("score_flush_blocks")) return rc;
+  }
+  return flush_clear(f, n_rows, overflow, s);
 }

@@ -57,6 +57,7 @@ struct PrefillArgs {
   float scale2;
   float* norm2;  // [count, q_heads] row normalisers in log2 units (sink included)
   int delay;     // pass 2 credits query i's keys k <= prefix_len + i - delay only
+  int block_shift;  // kind 4: log2 of the block size
 };
 
 // One 64-key tile of a wave: row-block rb's MFMAs for four 16-key blocks, then per logit one
@@ -310,6 +311,146 @@ __global__ __launch_bounds__(64 * pf::waves<PASS>()) void prefill_kernel(Prefill
 }
 
 // ---------------------------------------------------------------------------
+// Block counters of a chunk (score kind 4)
+// ---------------------------------------------------------------------------
+// The second pass for score kind 4 (TEX:197's block counters; no reference code). A
+// workgroup owns 16 queries and every KV head: wave g = KV head g, its MFMA rows (query,
+// head of g) as in pass 2, 8 row-blocks of 2 queries. Per 64-key tile the wave loads K_g of
+// the tile's keys straight into registers (the next tile's loads in flight during this one),
+// turns D = Q . K_g^T into probabilities with pass 1's normalisers and folds each (query,
+// key)'s maximum over g's heads into qk[query][key] in LDS with an unsigned max
+// (probabilities are non-negative, so their bit patterns order as the values do). Then per
+// (query, block) the maximum over the block's keys (a butterfly over the low lanes: blocks of
+// at most 64 aligned keys lie in one wave), summed over the 16 queries, goes to the block's
+// counter (KV head 0's score of its first slot) with one atomic per block and workgroup.
+// Query i credits the whole blocks of keys < prefix_len + i + 1 - delay.
+namespace pb {
+constexpr int QB = 16;          // queries per workgroup
+constexpr int RB = QB / 2;      // row-blocks per wave
+constexpr int WAVES = 8;        // wave g = KV head g
+constexpr int THREADS = 64 * WAVES;
+constexpr int KT = 64;          // keys per tile
+}  // namespace pb
+
+__global__ __launch_bounds__(pb::THREADS) void prefill_block_kernel(PrefillArgs a) {
+  using namespace pb;
+  __shared__ uint32_t qk[QB][KT];
+  __shared__ float part[WAVES][KT];
+  const int lane = threadIdx.x & 63;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int shift = a.block_shift;
+  // Heaviest query blocks (longest causal range) first.
+  const int64_t nqb = (a.count + QB - 1) / QB;
+  const int64_t qb0 = (nqb - 1 - int64_t(blockIdx.x)) * QB;
+  const int64_t last_q = (qb0 + QB < a.count ? qb0 + QB : a.count) - 1;
+  auto limit = [&](int64_t i) {  // credited keys of query i
+    return i < a.count ? block_step_limit(int(a.prefix_len + i + 1), a.delay, shift) : 0;
+  };
+  const int kend = limit(last_q);
+  if (kend <= 0) return;
+  for (int t = threadIdx.x; t < QB * KT; t += blockDim.x) qk[t / KT][t % KT] = 0u;
+  const bool live_wave = g < a.kv_heads;
+
+  // A fragments: row col of row-block rb is query qb0 + 2*rb + col/8, head g*8 + col%8, dims
+  // [8*grp, +8) and [32 + 8*grp, +8). This lane's D rows: query qb0 + 2*rb + grp/2, heads
+  // g*8 + 4*(grp%2) + r, with their normalisers (log2 units; +inf past the chunk) and limits.
+  bf16x8_t qa[RB][2];
+  f32x4_t nrm[RB];
+  int lim[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    qa[rb][0] = bf16x8_t{};
+    qa[rb][1] = bf16x8_t{};
+    const int64_t qi = qb0 + 2 * rb + (col >> 3);
+    if (live_wave && qi < a.count) {
+      const uint16_t* qp = a.q + qi * a.q_st + int64_t(g * pf::GROUP + (col & 7)) * a.q_sh + 8 * grp;
+      qa[rb][0] = as_bf16x8(*reinterpret_cast<const uint4*>(qp));
+      qa[rb][1] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 32));
+    }
+    const int64_t qd = qb0 + 2 * rb + (grp >> 1);
+    lim[rb] = limit(qd);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      nrm[rb][r] = live_wave && qd < a.count ? a.norm2[qd * a.q_heads + g * pf::GROUP + 4 * (grp & 1) + r] : INFINITY;
+  }
+  const auto kbase = as_global(a.k) + int64_t(live_wave ? g : 0) * a.kv_sh + 8 * grp;
+  auto load_k = [&](int t0, uint4 (&kf)[4][2]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int key = t0 + 16 * st + col;
+      const int64_t s = key < kend ? load_index_dyn(a.slots, a.slots_dtype, key) : 0;
+      const auto p = kbase + s * a.kv_ss;
+      kf[st][0] = gload16(p);
+      kf[st][1] = gload16(p + 32);
+    }
+  };
+  const int ntiles = (kend + KT - 1) / KT;
+  uint4 kf[4][2], kn[4][2];
+  if (live_wave) load_k(0, kf);
+  __syncthreads();  // qk cleared
+
+#pragma unroll 1
+  for (int ti = 0; ti < ntiles; ++ti) {
+    const int t0 = ti * KT;
+    if (live_wave) {
+      if (ti + 1 < ntiles) load_k(t0 + KT, kn);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        // Neither query of the row-block credits this tile (uniform; past the chunk a limit is 0).
+        const int rb_lim = limit(qb0 + 2 * rb) > limit(qb0 + 2 * rb + 1) ? limit(qb0 + 2 * rb) : limit(qb0 + 2 * rb + 1);
+        if (rb_lim <= t0) continue;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          f32x4_t d = mfma16x16x32(qa[rb][0], as_bf16x8(kf[st][0]), f32x4_t{0.f, 0.f, 0.f, 0.f});
+          d = mfma16x16x32(qa[rb][1], as_bf16x8(kf[st][1]), d);
+          const float e0 = fast_exp2(fmaf(d[0], a.scale2, -nrm[rb][0]));
+          const float e1 = fast_exp2(fmaf(d[1], a.scale2, -nrm[rb][1]));
+          const float e2 = fast_exp2(fmaf(d[2], a.scale2, -nrm[rb][2]));
+          const float e3 = fast_exp2(fmaf(d[3], a.scale2, -nrm[rb][3]));
+          const float mx = xor16_max(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
+          const int key = t0 + 16 * st + col;
+          if ((grp & 1) == 0 && key < lim[rb]) atomicMax(&qk[2 * rb + (grp >> 1)][16 * st + col], __float_as_uint(mx));
+        }
+      }
+    }
+    __syncthreads();
+    {
+      // Thread (q8 = t / 64, key = t % 64): queries q8 and q8 + 8, each reduced over its block.
+      const int key = threadIdx.x & (KT - 1), q8 = threadIdx.x >> 6;
+      float v0 = __uint_as_float(qk[q8][key]), v1 = __uint_as_float(qk[q8 + 8][key]);
+      qk[q8][key] = 0u;
+      qk[q8 + 8][key] = 0u;
+      for (int o = 1; o < (1 << shift); o <<= 1) {
+        v0 = fmaxf(v0, __shfl_xor(v0, o, kWave));
+        v1 = fmaxf(v1, __shfl_xor(v1, o, kWave));
+      }
+      part[q8][key] = v0 + v1;
+    }
+    __syncthreads();
+    if (threadIdx.x < KT) {
+      const int key = threadIdx.x;
+      if ((key & ((1 << shift) - 1)) == 0 && t0 + key < kend) {
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) tot += part[w][key];
+        if (tot > 0.f) {
+          const int64_t s = load_index_dyn(a.slots, a.slots_dtype, t0 + key);
+          unsafeAtomicAdd(&a.scores[s * a.sss], tot);
+        }
+      }
+    }
+    if (live_wave && ti + 1 < ntiles) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        kf[st][0] = kn[st][0];
+        kf[st][1] = kn[st][1];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Static regret diagnostic (pass 3)
 // ---------------------------------------------------------------------------
 constexpr int DIAG_MAX_SPECS = 8;
@@ -529,11 +670,16 @@ extern "C" int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_s
                                   void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
   if (head_dim != pf::D || kv_heads < 1 || q_heads != pf::GROUP * kv_heads)
     return gse_fail(GSE_ESHAPE, "prefill: need head_dim 64 and q_heads == 8 * kv_heads");
-  const int kind = mode & 0xff, delay = mode >> GSE_SCORE_DELAY_SHIFT;
-  if (kind != 1 && kind != 2) return gse_fail(GSE_EINVAL, "prefill: mode must be 1 (sum) or 2 (max)");
+  const int kind = mode & 0xf, block_shift = (mode >> GSE_SCORE_BLOCK_SHIFT) & 0xf;
+  const int delay = mode >> GSE_SCORE_DELAY_SHIFT;
+  if (kind != 1 && kind != 2 && kind != GSE_SCORE_KIND_BLOCK_STEP)
+    return gse_fail(GSE_EINVAL, "prefill: score kind must be 1 (sum), 2 (max) or 4 (block counters)");
+  if (kind != GSE_SCORE_KIND_BLOCK_STEP ? (mode & 0xf0) != 0 : block_shift > 6)
+    return gse_fail(GSE_EINVAL, "prefill: bad block size bits");
   if (delay < 0) return gse_fail(GSE_EINVAL, "prefill: negative score delay");
   if (count < 0 || prefix_len < 0 || total != prefix_len + count)
     return gse_fail(GSE_EINVAL, "prefill: total must equal prefix_len + count");
+  if (total >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "prefill: too many keys");
   if (count == 0) return GSE_OK;
   if (q_stride_t % 8 || q_stride_h % 8 || kv_stride_s % 8 || kv_stride_h % 8)
     return gse_fail(GSE_EINVAL, "prefill: strides must be multiples of 8 elements");
@@ -543,11 +689,19 @@ extern "C" int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_s
   PrefillArgs a = {static_cast<const uint16_t*>(q), q_stride_t, q_stride_h, count,
                    static_cast<const uint16_t*>(k_pool), kv_stride_s, kv_stride_h, slots, slots_dtype, total,
                    prefix_len, sinks, sinks_dtype, kind, scores, scores_stride_g, scores_stride_s, q_heads, kv_heads,
-                   sm_scale * kLog2e, static_cast<float*>(workspace), delay};
+                   sm_scale * kLog2e, static_cast<float*>(workspace), delay, block_shift};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t blocks = (count + pf::QB - 1) / pf::QB * kv_heads;
   if (blocks >= (int64_t(1) << 31)) return gse_fail(GSE_EINVAL, "prefill: chunk too large");
   const dim3 grid{static_cast<uint32_t>(blocks)};
+  if (kind == GSE_SCORE_KIND_BLOCK_STEP) {
+    if (kv_heads > pb::WAVES) return gse_fail(GSE_ESHAPE, "prefill: block counters need kv_heads <= 8");
+    hipLaunchKernelGGL((prefill_kernel<1, false>), grid, dim3(64 * pf::waves<1>()), 0, s, a);
+    if (int rc = gse_launch_check("prefill pass 1")) return rc;
+    hipLaunchKernelGGL(prefill_block_kernel, dim3(static_cast<uint32_t>((count + pb::QB - 1) / pb::QB)),
+                       dim3(pb::THREADS), 0, s, a);
+    return gse_launch_check("prefill block counters");
+  }
   if (kind == 2) {
     hipLaunchKernelGGL((prefill_kernel<1, true>), grid, dim3(64 * pf::waves<1>()), 0, s, a);
     if (int rc = gse_launch_check("prefill pass 1")) return rc;

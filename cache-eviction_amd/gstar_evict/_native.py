@@ -18,6 +18,7 @@ GSE_OK = 0
 I32, I64 = 0, 1
 F32, BF16 = 0, 1
 SCORE_NONE, SCORE_EAGER, SCORE_QUEUE = 0, 1, 2
+SCORE_KIND_BLOCK_STEP, SCORE_BLOCK_SHIFT = 4, 4
 POLICY_IDS = {"head_sum_2048": 1, "head_max_sum_2048": 2, "random_2048": 3,
               "random_reservoir_2048": 4, "prefix_sliding_2048": 5, "block_sum_2048": 6, "block_max_2048": 7}
 BOUNDARY_EVICTED, BOUNDARY_DEFERRED, BOUNDARY_ERR_HEADS, BOUNDARY_ERR_SWA, BOUNDARY_ERR_PACKED = 0, 2, 3, 4, 5
@@ -50,6 +51,8 @@ SIGNATURES = {
                         _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _i, _i, _p, _l, _p]),
     "gse_score_flush": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p, _p,
                              _p, _p, _i, _i, _i, _i, _i, _f, _p, _p]),
+    "gse_score_flush_blocks": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p,
+                                    _p, _p, _p, _i, _i, _i, _i, _i, _f, _p, _p]),
     "gse_decode_scores_from_lse": (_i, [_p, _l, _l, _p, _l, _l, _p, _p, _i, _p, _l, _l, _p, _i, _i, _p, _i,
                                         _p, _p, _i, _p, _l, _l, _i, _i, _i, _i, _f, _i, _p, _l, _p]),
     "gse_reservoir_scores": (_i, [_p, _i, _p, _p, _i, _i, _l, _l, _p, _p]),

@@ -19,9 +19,11 @@
  *                           slots*kv_heads, 1, kv_heads), so one page's scores fill whole lines
  *   table / req_to_token    int32 [rows, width]
  *   frontier / count / mode int32 [rows]; a mode word (mode_by_row[row], and the `mode`
- *                           of gse_prefill_scores) holds the score mode in bits 0-7 (1 sum,
- *                           2 max over a KV head's query heads, else no scores) and the
- *                           score delay in bits 8-30 (GSE_SCORE_DELAY_SHIFT)
+ *                           of gse_prefill_scores) holds the score kind in bits 0-3 (1 sum,
+ *                           2 max over a KV head's query heads, 4 block counters
+ *                           (GSE_SCORE_KIND_BLOCK_STEP), else no scores), log2 of the
+ *                           block size in bits 4-7 (kind 4 only) and the score delay in
+ *                           bits 8-30 (GSE_SCORE_DELAY_SHIFT)
  *   pos (per row)           int32 [full layers, kv_heads, count]
  */
 #ifndef GSTAR_EVICT_H
@@ -69,6 +71,20 @@ enum {
  * keys at least d positions older than the query. d = 0 is the reference's update.
  */
 #define GSE_SCORE_DELAY_SHIFT 8
+
+/*
+ * Block counters (score kind 4; no reference code: the reference report's ARC-AGI-3 block score,
+ * TEX:197, "a counter per block, scored by the maximum post-softmax attention over its four
+ * tokens and all query heads, counted after a delay of 128 tokens"). A block is 2^s aligned
+ * entries of the row's list (s = bits 4-7 of the word, 0..6); a block-policy boundary keeps
+ * whole position blocks in position order, so list blocks are position blocks. A query at list
+ * length lim credits the whole blocks of entries c < lim - d (d the delay): each such block's
+ * counter, KV head 0's score of the block's first slot, grows by the maximum over the block's
+ * keys and all query heads of the query's probability. The other slots of the block keep 0, so
+ * a block policy's sum or max over the block's scores is the counter.
+ */
+#define GSE_SCORE_KIND_BLOCK_STEP 4
+#define GSE_SCORE_BLOCK_SHIFT 4
 
 /* Boundary outcome written to device memory by gse_boundary. */
 enum {
@@ -186,7 +202,26 @@ int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stride_s, int64
                     int32_t* overflow, gse_stream_t stream);
 
 /*
- * decode_scores_from_lse — the reference's score update given an external
+ * score_flush_blocks — gse_score_flush for rows of score kind 4 (block counters,
+ * GSE_SCORE_KIND_BLOCK_STEP; no reference code, TEX:197): per queued step in queue order,
+ * each whole block of entries c < lim_i - delay adds to its counter (KV head 0's score of
+ * the block's first slot) the maximum over its keys and all query heads of
+ * exp(q_ih . k_c,g(h) * scale - norm_ih). Same arguments and queue semantics as
+ * gse_score_flush; each entry point folds only rows of its own kinds and empties the
+ * queues of every listed row, so a caller lists each row with the one that matches it.
+ */
+int gse_score_flush_blocks(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                           float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                           int64_t scores_stride_s, const int32_t* table, int64_t table_stride,
+                           const int32_t* req_to_token, int64_t r2t_stride, const int32_t* frontier,
+                           const int32_t* count, const int32_t* mode_by_row, const void* rows, int rows_dtype,
+                           int n_rows, int64_t max_len, const void* queue_q, const float* queue_norm,
+                           const int32_t* queue_lim, int32_t* queue_count, int rows_total, int queue_cap,
+                           int q_heads, int kv_heads, int head_dim, float sm_scale, int32_t* overflow,
+                           gse_stream_t stream);
+
+/*
+ * decode_scores_from_lse —the reference's score update given an external
  * decode kernel's split log-sum-exps. Replaces `_decode_scores` + `after_decode`
  * (R:155-224) exactly: the normaliser is rebuilt from attn_lse [bs, q_heads,
  * max_kv_splits] (strides in elements) over the valid splits of SGLang's layout
@@ -358,8 +393,11 @@ int gse_boundary_live_batch(float* scores, int layers, int64_t scores_stride_l, 
  * the score table (R:314-340, `_probabilities` + `_prefill_scores`):
  *   p[h, i, k] = exp(q_i,h . k_k * scale - logaddexp(logsumexp_k'(...), sink_h)),  k <= prefix_len + i
  *   scores[g, slots[k]] += sum_i (sum_{h in g} | max_{h in g}) p[h, i, k] [k <= prefix_len + i - delay]
- * with mode & 0xff (1 sum, 2 max) and the score delay of the mode word (the normaliser still
- * covers every key k <= prefix_len + i).
+ * with mode & 0xf (1 sum, 2 max) and the score delay of the mode word (the normaliser still
+ * covers every key k <= prefix_len + i). Kind 4 (block counters, GSE_SCORE_KIND_BLOCK_STEP)
+ * instead adds, per query i and whole block of keys < prefix_len + i + 1 - delay, the block's
+ * maximum over its keys and all query heads of p to the block's counter (KV head 0's score of
+ * the block's first slot); kv_heads <= 8 and a total below 2^31 keys.
  * q [count, q_heads, head_dim] bf16, keys gathered through slots (int64 or
  * int32, prefix slots then the chunk's own) from the pool. head_dim = 64,
  * q_heads = 8 * kv_heads. MFMA 16x16x32 bf16 tiles, two passes (row

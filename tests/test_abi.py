@@ -75,10 +75,34 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
 
 
 def test_score_word_layout_matches_the_header():
-    """The host packs a row's score delay above GSE_SCORE_DELAY_SHIFT, as the kernels unpack it."""
+    """The host packs a row's score delay above GSE_SCORE_DELAY_SHIFT and a block counter's
+    kind and block size as the header defines them, as the kernels unpack them."""
     from gstar_evict import requests
-    m = re.search(r"#define\s+GSE_SCORE_DELAY_SHIFT\s+(\d+)", open(HEADER).read())
-    assert m and int(m.group(1)) == requests.SCORE_DELAY_SHIFT
+    text = open(HEADER).read()
+    for name, value in (("GSE_SCORE_DELAY_SHIFT", requests.SCORE_DELAY_SHIFT),
+                        ("GSE_SCORE_KIND_BLOCK_STEP", requests.BLOCK_STEP),
+                        ("GSE_SCORE_BLOCK_SHIFT", requests.BLOCK_SHIFT)):
+        m = re.search(rf"#define\s+{name}\s+(\d+)", text)
+        assert m and int(m.group(1)) == value, name
+    cfg = dict(name="block_max_2048", budget=4096, prefix=64, recent=256, block=4, score_delay=128,
+               block_score="step_max")
+    entry = dict(mode=requests.policy_mode(cfg), cfg=cfg)
+    assert requests.score_word(entry) == 4 | 2 << 4 | 128 << 8
+
+
+def test_block_flush_rejects_bad_arguments_without_a_gpu():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    lib = _native.lib()
+    rc = lib.gse_score_flush_blocks(None, 12, 512, 64, None, 0, 0, 0, None, 0, None, 0, None, None, None, None, 0, 1,
+                                    100, None, None, None, None, 4, 65, 64, 8, 64, 0.125, None, None)
+    assert rc != 0 and b"queue_cap" in lib.gse_last_error()
+    rc = lib.gse_prefill_scores(None, 0, 0, 10, None, 0, 0, None, 0, 10, 0, None, 0, 4 | 7 << 4, None, 0, 0, 64, 8,
+                                64, 0.125, None, 0, None)
+    assert rc != 0 and b"block size" in lib.gse_last_error()
+    rc = lib.gse_prefill_scores(None, 0, 0, 10, None, 0, 0, None, 0, 10, 0, None, 0, 1 | 2 << 4, None, 0, 0, 64, 8,
+                                64, 0.125, None, 0, None)
+    assert rc != 0 and b"block size" in lib.gse_last_error()
 
 
 def test_row_descriptors_match_the_header_layout(tmp_path):

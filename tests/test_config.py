@@ -22,6 +22,14 @@ CONFIGS = [
     {"name": "block_sum_2048", "max_evicted_blocks": True},
     {"name": "block_sum_2048", "max_evicted_blocks": 2.0},
     {"name": "block_sum_2048", "block": 3},
+    {"name": "block_max_2048", "block": 4, "score_delay": 128, "max_evicted_blocks": 512,
+     "block_score": "step_max"},  # the report's counters (score kind 4)
+    {"name": "block_sum_2048", "block": 64, "block_score": "step_max"},
+    {"name": "block_sum_2048", "block": 128, "block_score": "step_max"},  # blocks of at most 64
+    {"name": "block_sum_2048", "shared": False, "block_score": "step_max"},  # counters are per layer
+    {"name": "block_sum_2048", "block_score": "position"},
+    {"name": "block_sum_2048", "block_score": "mean"},
+    {"name": "head_sum_2048", "block_score": "mean"},  # ignored: not a block policy
     {"name": "nope_2048"},
 ]
 
@@ -47,6 +55,14 @@ def test_score_word_carries_the_delay(requests):
     assert requests.score_word(requests.live_entry(REQ, {**BASE, "name": "random_2048"}, "live")) == 3
     bad = requests.live_entry(REQ, {**BASE, "name": "block_sum_2048", "score_delay": 999}, "live")
     assert requests.score_word(bad) == 0
+
+
+def test_score_word_of_block_counters(requests):
+    """Kind 4 with log2(block) in bits 4-7 and the delay from bit 8."""
+    cfg = {**BASE, "name": "block_sum_2048", "block": 16, "score_delay": 100, "block_score": "step_max"}
+    assert requests.score_word(requests.live_entry(REQ, cfg, "live")) == 4 | 4 << 4 | 100 << 8
+    cfg = {**BASE, "name": "block_max_2048", "block": 1, "block_score": "step_max"}
+    assert requests.score_word(requests.live_entry(REQ, cfg, "live")) == 4
 
 
 def test_boundary_budget_caps_the_evicted_blocks(requests):

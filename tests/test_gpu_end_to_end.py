@@ -83,6 +83,10 @@ CONFIGS = {
     # The reference report's settings: 4-token blocks scored by their maximum, delay 128, cap 512.
     "block_max_report": ({"name": "block_max_2048", "block": 4, "shared": True, "score_delay": 128,
                           "max_evicted_blocks": 512}, BUDGET),
+    # The same settings with the report's block score (TEX:197): per-block counters, each query
+    # adding the maximum over a whole, 128-position-old block's keys and all 64 query heads.
+    "block_counters_report": ({"name": "block_max_2048", "block": 4, "shared": True, "score_delay": 128,
+                               "max_evicted_blocks": 512, "block_score": "step_max"}, BUDGET),
 }
 
 
@@ -136,9 +140,15 @@ def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang, case):
         # Oracle chunk scores, 256 queries at a time (the probability tile stays small).
         pre = slot_of[:start].cpu().numpy()
         for lo in range(0, CHUNK, 256):
-            upd, sl = O.prefill_score_update(mode, q_all[start + lo:start + lo + 256].float().cpu().numpy(), kn,
-                                             sn, SCALE, 8, np.concatenate((pre, new[:lo].cpu().numpy())),
-                                             new[lo:lo + 256].cpu().numpy(), delay=delay)
+            chunk_q = q_all[start + lo:start + lo + 256].float().cpu().numpy()
+            seen = np.concatenate((pre, new[:lo].cpu().numpy()))
+            if mode == O.BLOCK_STEP:
+                upd, sl = O.prefill_block_step_update(chunk_q, kn, sn, SCALE, 8, seen, new[lo:lo + 256].cpu().numpy(),
+                                                      cfg["block"], delay=delay)
+                ost.scores[0][0, sl] += upd.astype(np.float32)
+                continue
+            upd, sl = O.prefill_score_update(mode, chunk_q, kn, sn, SCALE, 8, seen, new[lo:lo + 256].cpu().numpy(),
+                                             delay=delay)
             ost.scores[0][:, sl] += upd.astype(np.float32)
     entry = st.entries[ROW]
     assert [ev["after"] for ev in entry["events"]] == [CHUNK] == [ev["after"] for ev in oe["events"]]
@@ -194,7 +204,11 @@ def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang, case):
         if oe["count"]:
             tail = np.arange(oe["frontier"], p + 1)
             key_pos = np.concatenate((oe["pos"][0], np.broadcast_to(tail, (8, tail.size))), axis=1)
-        O.decode_scores_into(ost.scores[0], qn, ost.keys[0], res, norm, SCALE, mode, key_pos, p, delay)
+        if mode == O.BLOCK_STEP:  # shared blocks: every KV head holds the same positions
+            O.decode_block_step_into(ost.scores[0], qn, ost.keys[0], res, norm, SCALE, cfg["block"],
+                                     key_pos if key_pos.ndim == 1 else key_pos[0], p, delay)
+        else:
+            O.decode_scores_into(ost.scores[0], qn, ost.keys[0], res, norm, SCALE, mode, key_pos, p, delay)
         want_outs.append(want_o)
     ge.flush(st)
     got = torch.stack(outs).float().cpu().numpy()
@@ -202,3 +216,11 @@ def test_prompt_boundary_and_decode_match_the_oracle(fake_sglang, case):
     np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2)
     assert np.abs(got - want).mean() < 2e-3
     torch.testing.assert_close(st.scores.cpu(), torch.tensor(ost.scores), rtol=2e-3, atol=1e-6)
+    if mode == O.BLOCK_STEP:
+        # Counters sit in KV head 0 at the first slot of each whole, credited block only.
+        assert float(st.scores[0, 1:].abs().sum()) == 0.0
+        held = np.concatenate((entry["pos"][0, 0].cpu().numpy(), np.arange(entry["frontier"], PROMPT + STEPS)))
+        listed = np.concatenate((st.table[ROW, :entry["count"]].cpu().numpy(),
+                                 st.req_to_token[ROW, entry["frontier"]:PROMPT + STEPS].cpu().numpy()))
+        nonzero = st.scores[0, 0, torch.tensor(listed, device="cuda").long()].cpu().numpy() != 0
+        assert np.all(held[nonzero] % cfg["block"] == 0) and nonzero.sum() > 400  # of 576 blocks
