@@ -62,6 +62,9 @@ def parse(argv=None):
                    help="score delay of a --prefill block policy (the reference report's ARC-AGI-3 runs: 128)")
     p.add_argument("--prefill-cap", type=int, default=0,
                    help="evicted blocks per boundary of a --prefill block policy, 0 = no cap (the report: 512)")
+    p.add_argument("--prefill-block-score", default="position", choices=("position", "step_max"),
+                   help="block score of a --prefill block policy: accumulated position scores, or the report's "
+                        "per-block counters (step maximum over a block's keys and all query heads)")
     p.add_argument("--prefill", action="store_true",
                    help="time the chunked-prefill score tiles instead: 12 layers, 79,720-token prompt in "
                         "8192-token chunks, prefix capped at the 28,672-token budget (MFMA roofline)")
@@ -549,7 +552,7 @@ class PrefillWorkload:
         self.block_policy = args.prefill_policy in ("block_sum_2048", "block_max_2048")
         if self.block_policy:
             self.cfg.update(block=args.prefill_block, shared=True, score_delay=args.prefill_delay,
-                            max_evicted_blocks=args.prefill_cap)
+                            max_evicted_blocks=args.prefill_cap, block_score=args.prefill_block_score)
         self.starts = list(range(0, prompt, chunk))
 
     def run(self, timing=None, observe=None):
@@ -635,6 +638,8 @@ def prefill_bench(args, torch, ge):
         policy += f" {args.prefill_block}-token layer-shared blocks"
         policy += f", score delay {args.prefill_delay}" if args.prefill_delay else ""
         policy += f", at most {args.prefill_cap} blocks evicted per boundary" if args.prefill_cap else ""
+        if args.prefill_block_score == "step_max":
+            policy += ", per-block counters (step maximum over a block's keys and all query heads)"
     return {
         "metric": "chunked-prefill score tiles, TFLOP/s (one QK^T pass) and % of bf16 MFMA peak",
         "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 1,

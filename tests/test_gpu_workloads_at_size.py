@@ -261,6 +261,62 @@ def test_prefill_scores_of_the_last_queries_over_a_28k_prefix(ge, mode):
     torch.testing.assert_close(st.scores, expected, rtol=1e-3, atol=1e-6)
 
 
+def test_prefill_block_counters_of_the_last_queries_over_a_28k_prefix(ge):
+    """Block counters (the report's settings: 4-key blocks, delay 128) of the last 256 queries of
+    an 8192-query chunk over 28,672 resident keys, against the oracle in 32-query blocks."""
+    count, prefix_len, block, delay = 256, 28672 + 8192 - 256, 4, 128
+    _say(f"prefill block counters: {count} queries over {prefix_len} keys")
+    b, st, q, sinks, prefix, new = _prefill_case(ge, count, prefix_len, seed=11)
+    keys = b.token_to_kv_pool.get_key_buffer(1)
+    st.scores.zero_()
+    ge._prefill_scores(st, 0, 4 | 2 << 4 | delay << 8, layer(1), q, keys, sinks, prefix, new)
+    torch.cuda.synchronize()
+    kn, qn, sn = keys.float().cpu().numpy(), q.float().cpu().numpy(), sinks.float().cpu().numpy()
+    all_slots = torch.cat((prefix, new)).cpu().numpy()
+    credit = np.zeros(all_slots.size)
+    for lo in range(0, count, 32):
+        hi = min(lo + 32, count)
+        part, _ = O.prefill_block_step_update(qn[lo:hi], kn, sn, 0.125, G, all_slots[:prefix_len + lo],
+                                              all_slots[prefix_len + lo:prefix_len + hi], block, delay=delay)
+        credit[:prefix_len + hi] += part
+    expected = torch.zeros_like(st.scores)
+    expected[0, 0, torch.from_numpy(all_slots).cuda()] = torch.tensor(credit, dtype=torch.float32).cuda()
+    torch.testing.assert_close(st.scores, expected, rtol=1e-3, atol=1e-6)
+
+
+def test_prefill_block_counters_of_an_8k_chunk_over_a_28k_prefix_match_fp32(ge):
+    """All 8192 queries of a chunk over 28,672 resident keys (4-key blocks, delay 128) against an
+    fp32 torch computation of the same counters: per query, the causal probabilities with the
+    sink, the maximum over all 64 heads and over each whole block at least 128 keys old."""
+    count, prefix_len, block, delay = 8192, 28672, 4, 128
+    _say("prefill block counters: 8192 queries over 28672 + 8192 keys, fp32 reference")
+    b, st, q, sinks, prefix, new = _prefill_case(ge, count, prefix_len, seed=13)
+    keys = b.token_to_kv_pool.get_key_buffer(1)
+    st.scores.zero_()
+    ge._prefill_scores(st, 0, 4 | 2 << 4 | delay << 8, layer(1), q, keys, sinks, prefix, new)
+    slots = torch.cat((prefix, new))
+    got = st.scores[0, 0, slots].double()
+    kk = keys[slots].float().permute(1, 2, 0).contiguous()  # [G, D, T]
+    t = kk.shape[-1]
+    s = sinks.float().view(G, 8, 1, 1)
+    want = torch.zeros(t, dtype=torch.float64, device="cuda")
+    keys_at = torch.arange(t, device="cuda")
+    for lo in range(0, count, 128):
+        hi = lo + 128
+        qq = q[lo:hi].float().view(hi - lo, G, 8, D).permute(1, 2, 0, 3).contiguous()  # [G, 8, q, D]
+        logits = torch.matmul(qq, kk[:, None]) * 0.125  # [G, 8, q, T]
+        qpos = prefix_len + torch.arange(lo, hi, device="cuda")
+        logits.masked_fill_(keys_at[None, None, None, :] > qpos[None, None, :, None], -torch.inf)
+        norm = torch.logaddexp(torch.logsumexp(logits, -1, keepdim=True), s)
+        peak = torch.exp(logits - norm).amax(dim=(0, 1))  # [q, T]: the maximum over all 64 heads
+        whole = (qpos + 1 - delay) // block * block  # keys below this are in credited blocks
+        peak.masked_fill_(keys_at[None, :] >= whole[:, None], 0.0)
+        per_block = peak[:, :t // block * block].view(hi - lo, -1, block).amax(-1).double().sum(0)
+        want[torch.arange(0, t // block * block, block, device="cuda")] += per_block
+    torch.testing.assert_close(got, want, rtol=2e-3, atol=1e-6)
+    assert float(st.scores[0, 1:].abs().sum()) == 0.0
+
+
 def test_prefill_mass_of_an_8k_chunk_over_a_28k_prefix(ge):
     """Head-sum scores of a KV head add up to the non-sink probability mass of its 8 query heads
     over all 8192 queries of the chunk (a size-independent check)."""
@@ -286,19 +342,22 @@ def test_prefill_mass_of_an_8k_chunk_over_a_28k_prefix(ge):
     torch.testing.assert_close(got, total, rtol=1e-4, atol=1e-2)
 
 
-@pytest.mark.parametrize("variant", ["block16", "report"])
+@pytest.mark.parametrize("variant", ["block16", "report", "counters"])
 def test_block_eviction_flow_of_the_79720_token_prompt(ge, variant):
     """bench.py's --prefill flow (12 layers, 8192-token chunks, budget 512 + 4096 + 24,064): at
     every boundary each layer keeps the oracle's ``choose_blocks`` set (one set for all KV heads)
     computed from the GPU's own scores, and the relocated slots hold the claimed K, V, scores.
-    Variants: 16-token blocks (the default), and the reference report's ARC-AGI-3 settings
-    (4-token max blocks, score delay 128, at most 512 blocks evicted per boundary)."""
+    Variants: 16-token blocks (the default), the reference report's ARC-AGI-3 settings
+    (4-token max blocks, score delay 128, at most 512 blocks evicted per boundary), and those
+    settings with the report's block score (per-block counters, score kind 4)."""
     import bench
     from gstar_evict.requests import boundary_budget
     flags = ["--prefill", "--no-cpu-baseline"]
-    if variant == "report":
+    if variant in ("report", "counters"):
         flags += ["--prefill-policy", "block_max_2048", "--prefill-block", "4", "--prefill-delay", "128",
                   "--prefill-cap", "512"]
+    if variant == "counters":
+        flags += ["--prefill-block-score", "step_max"]
     args = bench.parse(flags)
     _say(f"prefill flow {variant}: building")
     w = bench.PrefillWorkload(args, torch, ge)
