@@ -570,18 +570,8 @@ using namespace gse;
 
 namespace {
 
-// Workgroups of the fused kernel: one per compute unit of the current device (cached).
-int fused_workgroups() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
+// Workgroups of the fused kernel: one per compute unit of the current device.
+int fused_workgroups() { return gse_device_cus(); }
 
 int check_decode_shape(int q_heads, int kv_heads, int head_dim) {
   if (head_dim != D) return gse_fail(GSE_ESHAPE, "decode: head_dim must be 64");

@@ -211,6 +211,196 @@ __global__ __launch_bounds__(fl::THREADS) void score_flush_kernel(FlushArgs a) {
   }
 }
 
+// Short queues (a few queued steps: rows that evict at every step, or a flush soon after a
+// boundary). Then the pass is bound by reading K, not by the exponentials, and how K is read
+// decides its speed. A workgroup owns one (layer, row) and walks chunks of 128 keys (grid
+// stride) with every KV head at once: wave g reads head g's 128 bytes of each of the chunk's
+// slot rows, so the 8 waves read whole 1 KiB rows together, as the decode kernel does. The
+// chunk's 8 head totals per key meet in LDS and leave as one 32-byte read-modify-write per slot
+// (the workgroup owns its keys for every head): no atomics, and each score row is written
+// once per flush. Up to 8 queued queries (every head's rows) stay in LDS for the whole walk;
+// longer queues are staged again per chunk, 8 queries at a time (correct, but the long-queue
+// kernel above reads them once).
+namespace fs {
+constexpr int WAVES = 8;  // wave g = KV head g
+constexpr int THREADS = WAVES * 64;
+constexpr int KEYS = 128;  // keys per chunk
+constexpr int SUB = KEYS / 16;
+constexpr int QG = 8;  // queued queries staged at once
+}  // namespace fs
+
+template <bool MAX_MODE>
+GSE_DEVICE void flush_short_group(const FlushArgs& a, const uint16_t* qs, const float* ns, const int* lims, int q0,
+                                  int count, int c0, const uint4 (&kf)[fs::SUB][2], float (&acc)[fs::SUB]) {
+  using namespace fs;
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+  const int g = threadIdx.x >> 6;
+  const int npairs = (count + 1) >> 1;
+  for (int pr = 0; pr < npairs; ++pr) {
+    const int la = lims[q0 + 2 * pr], lb = lims[q0 + 2 * pr + 1];
+    if (__builtin_amdgcn_readfirstlane(la > lb ? la : lb) <= c0) continue;  // both end before the chunk
+    // A rows: (query 2*pr + col/8, head g*8 + col%8); this lane's D rows: query 2*pr + grp/2,
+    // heads g*8 + 4*(grp%2) + r.
+    const uint16_t* qrow = qs + ((2 * pr + (col >> 3)) * 64 + g * fl::GROUP + (col & 7)) * fl::QROW + 8 * grp;
+    const bf16x8_t qa0 = as_bf16x8(*reinterpret_cast<const uint4*>(qrow));
+    const bf16x8_t qa1 = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + 32));
+    const int qi = 2 * pr + (grp >> 1);
+    const f32x4_t nrm = *reinterpret_cast<const f32x4_t*>(ns + qi * 64 + g * fl::GROUP + 4 * (grp & 1));
+    const int lim = lims[q0 + qi];
+#pragma unroll
+    for (int st = 0; st < SUB; ++st) {
+      f32x4_t d = mfma16x16x32(qa0, as_bf16x8(kf[st][0]), f32x4_t{0.f, 0.f, 0.f, 0.f});
+      d = mfma16x16x32(qa1, as_bf16x8(kf[st][1]), d);
+      acc[st] = flush_add<MAX_MODE, true>(d, nrm, a.scale2, c0 + 16 * st + col < lim, acc[st]);
+    }
+  }
+}
+
+// Grid (workgroups per (layer, row), n_rows, layers), fs::THREADS threads. A workgroup walks
+// chunks c0, c0 + stride, ... of its (layer, row) as a pipeline: while chunk i is computed, its
+// old score rows and chunk i+1's K rows and old score rows are in flight and chunk i+2's slot
+// indices are being read. After the MFMAs the 8 head totals of each key meet in LDS; wave w then
+// adds them to the score rows of the chunk's keys 16w..16w+15 (lanes 0-15 heads 0-3, lanes
+// 16-31 heads 4-7) and stores them.
+__global__ __launch_bounds__(fs::THREADS) void score_flush_short_kernel(FlushArgs a) {
+  using namespace fs;
+  __shared__ __attribute__((aligned(16))) uint16_t qs[QG * 64 * fl::QROW];
+  __shared__ __attribute__((aligned(16))) float ns[QG * 64];
+  __shared__ int lims[fl::MAX_QUEUE + 1];
+  __shared__ float red[WAVES][KEYS];
+
+  const int l = blockIdx.z;
+  const int64_t row = load_index_dyn(a.rows, a.rows_dtype, blockIdx.y);
+  const int word = a.mode[row];
+  const int md = score_kind(word);
+  if (md != 1 && md != 2) return;
+  const int64_t qbase = int64_t(l) * a.rows_total + row;  // (layer, row) queue index
+  int m = a.pcount[qbase];
+  m = m < a.cap ? m : a.cap;
+  if (m <= 0) return;
+  if (threadIdx.x < m) lims[threadIdx.x] = max(0, a.plim[qbase * a.cap + threadIdx.x] - score_delay(word));
+  if (threadIdx.x == m) lims[m] = 0;  // the missing query of an odd last pair credits nothing
+  __syncthreads();
+  int maxlim = 0;
+  for (int i = 0; i < m; ++i) maxlim = lims[i] > maxlim ? lims[i] : maxlim;
+  const int stride = gridDim.x * KEYS;
+  if (int(blockIdx.x) * KEYS >= maxlim) return;
+
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool live = g < a.kv_heads;
+  const int64_t cnt = a.count[row], fr = a.frontier[row];
+  auto slot_of = [&](int c) -> int32_t {
+    const int cc = c < maxlim ? c : maxlim - 1;
+    const int32_t s = cc < cnt ? a.table[row * a.table_stride + cc] : a.r2t[row * a.r2t_stride + fr + cc - cnt];
+    return c < maxlim ? s : 0;
+  };
+  const uint16_t* qsrc = a.pq + (qbase * a.cap) * a.q_heads * fl::D;
+  const float* nsrc = a.pnorm + (qbase * a.cap) * a.q_heads;
+  // The queued (query, head) rows of queries [q0, q0 + 8) and their normalisers (log2 units; a
+  // missing query gets zero rows and +inf, so its exponentials are 0).
+  auto stage = [&](int q0) {
+    for (int t = threadIdx.x; t < QG * a.q_heads * (fl::D / 8); t += blockDim.x) {
+      const int r = t / (fl::D / 8), piece = t % (fl::D / 8);
+      const int qi = r / a.q_heads, h = r % a.q_heads;
+      uint4 v = {0, 0, 0, 0};
+      if (q0 + qi < m) v = *reinterpret_cast<const uint4*>(qsrc + (int64_t(q0 + qi) * a.q_heads + h) * fl::D + 8 * piece);
+      *reinterpret_cast<uint4*>(qs + (qi * 64 + h) * fl::QROW + 8 * piece) = v;
+    }
+    for (int t = threadIdx.x; t < QG * a.q_heads; t += blockDim.x) {
+      const int qi = t / a.q_heads, h = t % a.q_heads;
+      ns[qi * 64 + h] = q0 + qi < m ? nsrc[int64_t(q0 + qi) * a.q_heads + h] * kLog2e : INFINITY;
+    }
+  };
+  const bool one_group = m <= QG;
+  if (one_group) stage(0);
+  const auto kp = as_global(static_cast<const uint16_t*>(a.k_pools[l])) + int64_t(live ? g : 0) * a.kv_sh + 8 * grp;
+  float* sbase = a.scores + int64_t(l) * a.ssl;
+  // A slot's 8 head scores as one 32-byte row (the runtime's layout) when aligned for it; else
+  // each head's score separately.
+  const bool rows32 = a.ssg == 1 && a.sss == 8 && a.kv_heads == 8 && (reinterpret_cast<uintptr_t>(sbase) & 15) == 0;
+  // This lane's share of the score update: key 16*g + col of the chunk, heads 4*half..+3
+  // (lanes 0-31; lanes 32-63 idle there).
+  const int half = (lane >> 4) & 1;
+  const bool updater = lane < 32;
+
+  int32_t sl[SUB], sl_next[SUB];
+  uint4 kf[SUB][2];
+  f32x4_t old = {0.f, 0.f, 0.f, 0.f}, old_next = {0.f, 0.f, 0.f, 0.f};
+  auto load_rows = [&](const int32_t (&s)[SUB], int c, f32x4_t& o) {
+#pragma unroll
+    for (int st = 0; st < SUB; ++st) {
+      if (live) {
+        const auto p = kp + uint64_t(uint32_t(s[st])) * uint64_t(a.kv_ss);
+        kf[st][0] = gload16(p);
+        kf[st][1] = gload16(p + 32);
+      }
+    }
+    if (rows32 && updater && c + 16 * g + col < maxlim)
+      o = *reinterpret_cast<const f32x4_t*>(sbase + uint64_t(uint32_t(s[g])) * 8 + 4 * half);
+  };
+  int c0 = blockIdx.x * KEYS;
+#pragma unroll
+  for (int st = 0; st < SUB; ++st) sl[st] = slot_of(c0 + 16 * st + col);
+  load_rows(sl, c0, old);
+#pragma unroll
+  for (int st = 0; st < SUB; ++st) sl_next[st] = c0 + stride < maxlim ? slot_of(c0 + stride + 16 * st + col) : 0;
+
+  for (; c0 < maxlim; c0 += stride) {
+    float acc[SUB];
+#pragma unroll
+    for (int st = 0; st < SUB; ++st) acc[st] = 0.f;
+    for (int q0 = 0; q0 < m; q0 += QG) {
+      if (!one_group) {
+        __syncthreads();
+        stage(q0);
+      }
+      __syncthreads();  // staged rows visible; the previous chunk's totals read
+      if (live) {
+        const int count = m - q0 < QG ? m - q0 : QG;
+        if (md == 2)
+          flush_short_group<true>(a, qs, ns, lims, q0, count, c0, kf, acc);
+        else
+          flush_short_group<false>(a, qs, ns, lims, q0, count, c0, kf, acc);
+      }
+    }
+    if (live) {
+#pragma unroll
+      for (int st = 0; st < SUB; ++st) {
+        // Sum mode: lanes of all four groups hold partial sums. Max mode: groups 0/1 hold the
+        // even queries' sums (twice), 2/3 the odd ones'.
+        const float tot = md == 2 ? xor32_sum(acc[st]) : xor32_sum(xor16_sum(acc[st]));
+        if (grp == 0) red[g][16 * st + col] = tot;
+      }
+    }
+    // The next chunk's rows go out now (K is free once the MFMAs have read it).
+    const int c1 = c0 + stride;
+    const int32_t my_slot = sl[g];
+    if (c1 < maxlim) {
+      load_rows(sl_next, c1, old_next);
+#pragma unroll
+      for (int st = 0; st < SUB; ++st) {
+        sl[st] = sl_next[st];
+        sl_next[st] = c1 + stride < maxlim ? slot_of(c1 + stride + 16 * st + col) : 0;
+      }
+    }
+    __syncthreads();  // every head's totals of this chunk in LDS
+    const int key = 16 * g + col;
+    if (updater && c0 + key < maxlim) {
+      if (rows32) {
+        f32x4_t v = old;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) v[h] += red[4 * half + h][key];
+        *reinterpret_cast<f32x4_t*>(sbase + uint64_t(uint32_t(my_slot)) * 8 + 4 * half) = v;
+      } else if (half == 0) {
+        float* p = sbase + uint64_t(uint32_t(my_slot)) * a.sss;
+        for (int h = 0; h < a.kv_heads; ++h) p[h * a.ssg] += red[h][key];
+      }
+    }
+    old = old_next;
+  }
+}
+
 // Kind 4 (block counters; TEX:197, no reference code). A workgroup owns (layer, row, 128 keys)
 // for every KV head: wave g keeps K_g of the 128 keys in registers and runs, per pair of queued
 // queries, D = [Q_i; Q_i+1] . K_g^T (the query rows of g's heads, read from the queue), so a lane
@@ -395,6 +585,41 @@ extern "C" int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stri
     hipLaunchKernelGGL(score_flush_kernel, dim3(chunks, unsigned(n_rows), unsigned(layers * kv_heads)), dim3(THREADS),
                        0, s, f);
     if (int rc = gse_launch_check("score_flush")) return rc;
+  }
+  return flush_clear(f, n_rows, overflow, s);
+}
+
+extern "C" int gse_score_flush_short(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                                     float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                                     int64_t scores_stride_s, const int32_t* table, int64_t table_stride,
+                                     const int32_t* req_to_token, int64_t r2t_stride, const int32_t* frontier,
+                                     const int32_t* count, const int32_t* mode_by_row, const void* rows,
+                                     int rows_dtype, int n_rows, int64_t max_len, const void* pend_q,
+                                     const float* pend_norm, const int32_t* pend_lim, int32_t* pend_count,
+                                     int rows_total, int queue_cap, int q_heads, int kv_heads, int head_dim,
+                                     float sm_scale, int32_t* overflow, gse_stream_t stream) {
+  FlushArgs f = {};
+  if (int rc = flush_args(f, k_pools, layers, kv_stride_s, kv_stride_h, scores, scores_stride_l, scores_stride_g,
+                          scores_stride_s, table, table_stride, req_to_token, r2t_stride, frontier, count,
+                          mode_by_row, rows, rows_dtype, n_rows, max_len, pend_q, pend_norm, pend_lim, pend_count,
+                          rows_total, queue_cap, q_heads, kv_heads, head_dim, sm_scale))
+    return rc;
+  if (n_rows == 0 || layers == 0) return GSE_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t chunks = (max_len + fs::KEYS - 1) / fs::KEYS;
+  if (chunks) {
+    // Workgroups per (layer, row) pair: each walks its pair's chunks with that stride, one
+    // workgroup resident per CU. Pick the count that minimises rounds of resident workgroups
+    // times chunks per walk (for lists of max_len keys), the smallest on ties.
+    const int64_t pairs = int64_t(n_rows) * layers, cus = gse_device_cus();
+    int64_t per = 1, best = -1;
+    for (int64_t p = 1; p <= (chunks < 64 ? chunks : 64); ++p) {
+      const int64_t cost = ((p * pairs + cus - 1) / cus) * ((chunks + p - 1) / p);
+      if (best < 0 || cost < best) best = cost, per = p;
+    }
+    hipLaunchKernelGGL(score_flush_short_kernel, dim3(unsigned(per), unsigned(n_rows), unsigned(layers)),
+                       dim3(fs::THREADS), 0, s, f);
+    if (int rc = gse_launch_check("score_flush_short")) return rc;
   }
   return flush_clear(f, n_rows, overflow, s);
 }

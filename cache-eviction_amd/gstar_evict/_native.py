@@ -51,6 +51,8 @@ SIGNATURES = {
                         _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _i, _i, _p, _l, _p]),
     "gse_score_flush": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p, _p,
                              _p, _p, _i, _i, _i, _i, _i, _f, _p, _p]),
+    "gse_score_flush_short": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p,
+                                   _p, _p, _p, _i, _i, _i, _i, _i, _f, _p, _p]),
     "gse_score_flush_blocks": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p,
                                     _p, _p, _p, _i, _i, _i, _i, _i, _f, _p, _p]),
     "gse_decode_scores_from_lse": (_i, [_p, _l, _l, _p, _l, _l, _p, _p, _i, _p, _l, _l, _p, _i, _i, _p, _i,

@@ -202,6 +202,24 @@ int gse_score_flush(void* const* k_pools, int layers, int64_t kv_stride_s, int64
                     int32_t* overflow, gse_stream_t stream);
 
 /*
+ * score_flush_short — gse_score_flush for short queues (a few steps per row, e.g. rows that
+ * evict at every step): same arguments, result and queue handling. No reference counterpart
+ * (the reference adds each step eagerly, R:189-200). Each workgroup reads every KV head of its
+ * keys at once and writes a slot's score row with one read-modify-write (no atomics); up to 8
+ * queued steps per row are read once, longer queues again per 128 keys, so for full queues
+ * gse_score_flush is the faster choice.
+ */
+int gse_score_flush_short(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                          float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                          int64_t scores_stride_s, const int32_t* table, int64_t table_stride,
+                          const int32_t* req_to_token, int64_t r2t_stride, const int32_t* frontier,
+                          const int32_t* count, const int32_t* mode_by_row, const void* rows, int rows_dtype,
+                          int n_rows, int64_t max_len, const void* queue_q, const float* queue_norm,
+                          const int32_t* queue_lim, int32_t* queue_count, int rows_total, int queue_cap,
+                          int q_heads, int kv_heads, int head_dim, float sm_scale, int32_t* overflow,
+                          gse_stream_t stream);
+
+/*
  * score_flush_blocks — gse_score_flush for rows of score kind 4 (block counters,
  * GSE_SCORE_KIND_BLOCK_STEP; no reference code, TEX:197): per queued step in queue order,
  * each whole block of entries c < lim_i - delay adds to its counter (KV head 0's score of

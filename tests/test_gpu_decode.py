@@ -169,6 +169,45 @@ def test_queue_over_steps_equals_eager():
     torch.testing.assert_close(results[True], results[False], rtol=1e-5, atol=1e-8)
 
 
+@pytest.mark.parametrize("steps,delay,kv_heads", [(1, 0, 8), (5, 0, 8), (8, 64, 8), (13, 0, 8), (3, 7, 4)])
+def test_short_and_long_queue_flushes_agree(monkeypatch, steps, delay, kv_heads):
+    """The short-queue flush (a workgroup reads every KV head of its keys, one score-row write
+    per slot) and the long-queue flush fold the same queued steps (rows of sum and max mode,
+    growing lists) to the same scores, and both equal the eager per-step update. 13 steps take
+    the short kernel's restaging path; 4 KV heads its per-head score writes."""
+    from gstar_evict import attention
+    heads = 8 * kv_heads
+    results = {}
+    for which in ("long", "short", "eager"):
+        monkeypatch.setattr(attention, "SHORT_QUEUE", 64 if which == "short" else -1)
+        ge.STATE = None
+        b = backend(gen=torch.Generator().manual_seed(1), kv_heads=kv_heads)
+        st = ge.state(b)
+        st.score_mode = "eager" if which == "eager" else "queue"
+        st.mode[1], st.mode[2] = 1 | delay << 8, 2 | delay << 8
+        base = [100, 1301]
+        perm = (torch.randperm(19999, generator=torch.Generator().manual_seed(2))[:3000] + 1).cuda()
+        sinks = torch.randn(heads, generator=torch.Generator().manual_seed(5)).cuda()
+        for t in range(steps):
+            q = torch.randn((2, heads, 64), generator=torch.Generator().manual_seed(10 + t)).to(torch.bfloat16).cuda()
+            lens = [base[0] + t, base[1] + t]
+            idx = torch.cat((perm[:lens[0]], perm[1500:1500 + lens[1]]))
+            indptr = torch.tensor([0, lens[0], lens[0] + lens[1]], dtype=torch.int32, device="cuda")
+            b.forward_metadata = SimpleNamespace(kv_indptr=indptr, kv_indices=idx)
+            fb = SimpleNamespace(out_cache_loc=idx[indptr[1:].long() - 1], req_pool_indices=torch.tensor(
+                [1, 2], device="cuda"), seq_lens_cpu=torch.tensor(lens))
+            o = torch.empty((2, heads, 64), dtype=torch.bfloat16, device="cuda")
+            lay = layer(1, heads=heads, kv_heads=kv_heads)
+            ge.decode(b, q.reshape(2, -1), lay, fb, sinks, o.reshape(2, -1))
+        st.req_to_token[1, :base[0] + steps] = perm[:base[0] + steps].int()
+        st.req_to_token[2, :base[1] + steps] = perm[1500:1500 + base[1] + steps].int()
+        ge.flush(st)
+        results[which] = st.scores.clone()
+    assert float(results["long"].abs().sum()) > 0
+    torch.testing.assert_close(results["short"], results["long"], rtol=1e-6, atol=1e-9)
+    torch.testing.assert_close(results["short"], results["eager"], rtol=1e-5, atol=1e-8)
+
+
 @pytest.mark.parametrize("mode,delay", [(1, 0), (2, 0), (1, 64)])
 def test_after_decode_rebuilds_normaliser_from_split_lse(mode, delay):
     """T:48-78 with SGLang's split LSE layout (splits [1, 5, 8]) produced by the oracle; with a
