@@ -53,6 +53,7 @@ def parse(argv=None):
     p.add_argument("--kernel-reps", type=int, default=20, help="launches timed per layer for the roofline")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--eager", action="store_true", help="score each step eagerly (second K pass per step)")
+    p.add_argument("--pairs", type=int, default=200, help="off/on pairs per size and policy of --decode-latency")
     p.add_argument("--decode-latency", action="store_true",
                    help="bs=1 decode layer latency at 8K/16K/32K resident (the reference's published shape)")
     p.add_argument("--prefill-policy", default="block_sum_2048",
@@ -673,7 +674,8 @@ def decode_latency_bench(args, torch, ge):
       queued     - head_sum: attention, the step queued, plus the flush of a full 64-step queue
                    for this layer amortised over its 64 steps (timed separately);
       eager      - head_sum with the score added in the same call (a second pass over K).
-    """
+    Then, per size and policy (head_sum, head_max_sum), the reference's paired off/on protocol
+    (``paired_timing``, TM:58-87): per-call event pairs, launch path included."""
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(args.seed)
     sizes = (8192, 16384, 32768)
@@ -755,6 +757,8 @@ def decode_latency_bench(args, torch, ge):
                 us += flush_us / st.queue_cap
             out[f"{mode_name}_us"] = round(us, 2)
         out["attention_GB_s"] = round((2052 * n + 16512) / (out["attention_us"] * 1e-6) / 1e9, 1)
+        out["paired"] = [paired_timing(torch, ge, backend, mode, q, lay, sinks, o, order, n, policy, args)
+                         for policy, mode in (("head_sum_2048", 1), ("head_max_sum_2048", 2))]
         results.append(out)
     return {
         "metric": "bs=1 decode layer latency (gpt-oss-20b full-attention shape), us",
@@ -766,6 +770,52 @@ def decode_latency_bench(args, torch, ge):
         "reference_gb10": {"8192": {"attention_us": 58.9, "with_scores_us": 83.9},
                            "16384": {"attention_us": 150.0, "with_scores_us": 192.9}},
     }
+
+
+def paired_timing(torch, ge, backend, mode, q, lay, sinks, o, order, n, policy, args):
+    """The reference's paired protocol (TM:58-87) on one full-attention layer at bs=1: "off" is
+    the decode attention alone, "on" the same call with the policy's score update added before
+    it returns (the reference's per-step `after_decode`; here the eager second pass over K).
+    Each sample is one call between two events with a synchronize on each side, the scores are
+    zeroed outside the timed region, pairs alternate their order, and 20 warm-up pairs run
+    first. Reports the means, the paired deltas and the overhead."""
+    import statistics
+    dev = q.device
+    ge.STATE = None
+    st = ge.state(backend)
+    st.score_mode = "eager"
+    rows = torch.tensor([1], device=dev)
+    st.req_to_token[1, :n] = order[:n].int()
+    kv_indices = torch.zeros(n, dtype=torch.int32, device=dev)
+    ge.fill(backend, 1, torch.tensor([n], device=dev), rows, kv_indices)
+    backend.forward_metadata = SimpleNamespace(kv_indptr=backend.kv_indptr[:2], kv_indices=kv_indices)
+    fb = SimpleNamespace(out_cache_loc=order[n - 1:n], req_pool_indices=rows, seq_lens_cpu=[n])
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(on):
+        st.mode[1] = mode if on else 0
+        st.scores.zero_()
+        torch.cuda.synchronize()
+        start.record()
+        ge.decode(backend, q.view(1, -1), lay, fb, sinks, o.view(1, -1))
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end)
+
+    for _ in range(20):
+        timed(False), timed(True)
+    pairs = []
+    for i in range(args.pairs):
+        order_i = (False, True) if i % 2 == 0 else (True, False)
+        sample = {on: timed(on) for on in order_i}
+        pairs.append((sample[False], sample[True]))
+    deltas = [b - a for a, b in pairs]
+    off, on = statistics.mean(a for a, _ in pairs), statistics.mean(b for _, b in pairs)
+    return {"policy": policy, "pairs": len(pairs), "warmup_pairs": 20, "synchronization": "hip_event_per_sample",
+            "off_us": round(1000 * off, 2), "on_us": round(1000 * on, 2), "extra_us": round(1000 * (on - off), 2),
+            "paired_delta_mean_us": round(1000 * statistics.mean(deltas), 2),
+            "paired_delta_stdev_us": round(1000 * statistics.stdev(deltas), 2),
+            "overhead_percent": round(100 * (on - off) / off, 1)}
 
 
 def replay_bench(args, torch, ge):

@@ -12,8 +12,21 @@ from fakes import FULL, backend, layer
 
 pytestmark = pytest.mark.gpu
 
+# Each spec takes its own protection (T:240-244): random_2048 protects 64 prefix and 16 recent
+# positions, the others 16 and 64 (prefix_sliding: 16 and 884).
 SPECS = {"head_sum_2048": (900, 16, 64), "head_max_sum_2048": (900, 16, 64),
-         "prefix_sliding_2048": (900, 16, 884), "random_reservoir_2048": (900, 16, 64)}
+         "prefix_sliding_2048": (900, 16, 884), "random_reservoir_2048": (900, 16, 64),
+         "random_2048": (900, 64, 16)}
+
+
+def _random_draws(seed, n, layers, kv_heads, held):
+    """random_2048's draws of a diagnostic spec at boundary n: torch's device generator seeded
+    with R:573-575's (seed * 1000003 + n * 31 + j) & 0x7FFFFFFF, j the spec's index."""
+    j = list(SPECS).index("random_2048")
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed((seed * 1000003 + n * 31 + j) & 0x7FFFFFFF)
+    draws = torch.rand((layers, kv_heads, held), generator=generator, device="cuda", dtype=torch.float64)
+    return {j: draws.cpu().numpy()}
 
 
 @pytest.fixture(autouse=True)
@@ -50,7 +63,8 @@ def test_lost_mass_and_score_tables_match_the_oracle(runtime):
             ge._diagnose(st, e, index, layer(lid), queries[lid][lo:hi], b.token_to_kv_pool.get_key_buffer(lid),
                          sinks[lid], slots, lo)
             O.diagnose(oe, index, len(FULL), queries[lid][lo:hi].float().cpu().numpy(), keys_np[lid],
-                       sinks[lid].cpu().numpy(), 0.125, kv_heads, lo)
+                       sinks[lid].cpu().numpy(), 0.125, kv_heads, lo,
+                       random_scores=_random_draws(5, lo, len(FULL), kv_heads, lo) if lo else None)
         torch.cuda.synchronize()
         assert e["error"] is None
         assert np.array_equal(e["resident"].cpu().numpy(), oe["resident"]), (lo, hi)

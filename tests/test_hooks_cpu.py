@@ -115,3 +115,13 @@ def test_errors_keep_the_row_inert_and_a_new_owner_starts_clean(hooks):
     _extend(ge, _req("b", 1, 0, 2048, {"gstar_replay": CFG}))  # the row changes hands
     e = st.entries[1]
     assert e["key"] == "b" and e["kind"] == "replay" and e["error"] is None and int(st.mode[1]) == 1
+
+
+def test_diagnostic_specs_take_their_own_protection(hooks):
+    """T:240-244: each comma-separated spec keeps its own name, budget, prefix and recent."""
+    ge, _, _ = hooks
+    req = SimpleNamespace(rid="r", session=None, origin_input_ids=[0] * 10)
+    e = ge._diagnostic_entry(req, {"policies": "random_2048:8192:2048:2048,prefix_sliding_2048:8192:2048:6144"},
+                             "cpu", 12, 8)
+    assert e["specs"] == [("random_2048", 8192, 2048, 2048), ("prefix_sliding_2048", 8192, 2048, 6144)]
+    assert tuple(e["resident"].shape) == (2, 12, 8, 10) and bool(e["resident"].all())
