@@ -10,7 +10,8 @@
  *
  * Reference paths below are relative to the tonghuikang/cache-eviction
  * repository: R = code/cache_eviction/sglang_evict_runtime.py,
- * C = code/cache_eviction/core.py, T = code/tests/test_sglang_evict.py.
+ * C = code/cache_eviction/core.py, T = code/tests/test_sglang_evict.py, TEX = source.tex (the
+ * reference report, which describes the block variant that the reference ships no code for).
  *
  * Layouts (the reference's, R:89-110):
  *   K/V pool of one layer   bf16 [slots, kv_heads, head_dim], head_dim contiguous
