@@ -322,7 +322,7 @@ __global__ __launch_bounds__(fs::THREADS) void score_flush_short_kernel(FlushArg
   // This lane's share of the score update: key 16*g + col of the chunk, heads 4*half..+3
   // (lanes 0-31; lanes 32-63 idle there).
   const int half = (lane >> 4) & 1;
-  const bool updater = lane < 32;
+  const bool updater = lane < 32 && g < SUB;
 
   int32_t sl[SUB], sl_next[SUB];
   uint4 kf[SUB][2];
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(fs::THREADS) void score_flush_short_kernel(FlushArg
       }
     }
     if (rows32 && updater && c + 16 * g + col < maxlim)
-      o = *reinterpret_cast<const f32x4_t*>(sbase + uint64_t(uint32_t(s[g])) * 8 + 4 * half);
+      o = *reinterpret_cast<const f32x4_t*>(sbase + uint64_t(uint32_t(s[g < SUB ? g : 0])) * 8 + 4 * half);
   };
   int c0 = blockIdx.x * KEYS;
 #pragma unroll
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(fs::THREADS) void score_flush_short_kernel(FlushArg
     }
     // The next chunk's rows go out now (K is free once the MFMAs have read it).
     const int c1 = c0 + stride;
-    const int32_t my_slot = sl[g];
+    const int32_t my_slot = sl[g < SUB ? g : 0];
     if (c1 < maxlim) {
       load_rows(sl_next, c1, old_next);
 #pragma unroll

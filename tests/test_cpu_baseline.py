@@ -117,3 +117,12 @@ def test_benchmark_rows_are_valid_boundary_inputs(n):
     assert ls["used"].numel() == budget + n - row["frontier"]
     assert (ls["req_to_token"][row["frontier"] - recent:n] > 0).all()
     assert _boundary_both(ls, 1, budget, prefix, recent, n - 256, n)
+
+
+def test_bench_reads_the_profiled_decode_traffic():
+    """The bench line's roofline.traffic comes from the committed decode profile summary: it
+    must parse, and sit within 5 % above the launch's algorithmic bytes at the default workload
+    (about 1.944 GB)."""
+    traffic = bench.measured_traffic()
+    assert traffic is not None
+    assert 1.944e9 <= traffic <= 1.05 * 1.944e9
