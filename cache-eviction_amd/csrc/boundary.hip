@@ -1223,9 +1223,6 @@ __global__ __launch_bounds__(256) void relocate_rows_kernel(BndArgs a) {
 // the first barrier all of them are resident, so a later wait cannot outlast the limit in
 // practice; if one did, it marks the boundary GSE_BOUNDARY_ERR_RELOCATE, which the host raises.
 
-// The wave's loaded registers are in use here: the compiler waits for exactly these loads.
-GSE_DEVICE void landed(const uint4& x) { asm volatile("" ::"v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w)); }
-GSE_DEVICE void landed(float x) { asm volatile("" ::"v"(x)); }
 
 // Arrival at phase `phase`'s barrier, after every wave of the workgroup has its loads. Counters
 // 64 words (256 bytes) apart: the top one, then group k's (workgroups k, k + 8, ...); a group's

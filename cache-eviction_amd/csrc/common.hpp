@@ -61,6 +61,11 @@ GSE_DEVICE f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
 
 GSE_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The wave's loaded registers are in use here: the compiler waits for exactly these loads.
+GSE_DEVICE void landed(const uint4& x) { asm volatile("" ::"v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w)); }
+GSE_DEVICE void landed(float x) { asm volatile("" ::"v"(x)); }
+GSE_DEVICE void landed(const bf16x8_t& x) { landed(__builtin_bit_cast(uint4, x)); }
+
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 
 // ds_read_b64_tr_b16: in each 16-lane group, source lane j supplies 4 consecutive

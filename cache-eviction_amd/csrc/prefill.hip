@@ -241,6 +241,16 @@ __global__ __launch_bounds__(64 * pf::waves<PASS>()) void prefill_kernel(Prefill
 #pragma unroll 1
   for (int ti = 0; ti < ntiles; ++ti) {
     const int64_t t0 = int64_t(ti) * KT;
+    // The fragments loaded before the loop are in registers by now; saying so here, before the
+    // next tile's loads go out, keeps the tile's first MFMA from waiting for those loads too.
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      landed(qa[rb][0]);
+      landed(qa[rb][1]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (PASS == 2) landed(ref[rb][r]);
+    }
     if (loader && ti + 1 < ntiles) load_tile(t0 + KT, x0, x1);  // in flight during this tile's compute
     if (wave_live && t0 < wave_kend) {
       const uint16_t* kt = ktile[ti & 1];
@@ -330,16 +340,20 @@ constexpr int RB = QB / 2;      // row-blocks per wave
 constexpr int WAVES = 8;        // wave g = KV head g
 constexpr int THREADS = 64 * WAVES;
 constexpr int KT = 64;          // keys per tile
+constexpr int RING = 16;        // tiles of block credits held in LDS before they go to the scores
 }  // namespace pb
 
+template <typename IdxT>
 __global__ __launch_bounds__(pb::THREADS) void prefill_block_kernel(PrefillArgs a) {
   using namespace pb;
   __shared__ uint32_t qk[QB][KT];
   __shared__ float part[WAVES][KT];
+  __shared__ float ring[RING][KT];  // block credits of RING tiles, added to the scores once per ring
   const int lane = threadIdx.x & 63;
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const int shift = a.block_shift;
+  const IdxT* slots = static_cast<const IdxT*>(a.slots);
   // Heaviest query blocks (longest causal range) first.
   const int64_t nqb = (a.count + QB - 1) / QB;
   const int64_t qb0 = (nqb - 1 - int64_t(blockIdx.x)) * QB;
@@ -350,6 +364,7 @@ __global__ __launch_bounds__(pb::THREADS) void prefill_block_kernel(PrefillArgs 
   const int kend = limit(last_q);
   if (kend <= 0) return;
   for (int t = threadIdx.x; t < QB * KT; t += blockDim.x) qk[t / KT][t % KT] = 0u;
+  for (int t = threadIdx.x; t < RING * KT; t += blockDim.x) ring[t / KT][t % KT] = 0.f;
   const bool live_wave = g < a.kv_heads;
 
   // A fragments: row col of row-block rb is query qb0 + 2*rb + col/8, head g*8 + col%8, dims
@@ -374,27 +389,47 @@ __global__ __launch_bounds__(pb::THREADS) void prefill_block_kernel(PrefillArgs 
     for (int r = 0; r < 4; ++r)
       nrm[rb][r] = live_wave && qd < a.count ? a.norm2[qd * a.q_heads + g * pf::GROUP + 4 * (grp & 1) + r] : INFINITY;
   }
+  // The K rows of tile i + 1 are in flight while tile i computes, and their slot indices were
+  // read a tile before that, so a tile's K loads go out together and its compute waits on
+  // nothing issued during it. The two register sets alternate between tiles.
   const auto kbase = as_global(a.k) + int64_t(live_wave ? g : 0) * a.kv_sh + 8 * grp;
-  auto load_k = [&](int t0, uint4 (&kf)[4][2]) {
+  // The indices stay as loaded until the next tile turns them into addresses (using them at
+  // once would make the compiler wait for every load in flight, K included).
+  auto load_idx = [&](int t0, IdxT (&s)[4]) {
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int key = t0 + 16 * st + col;
-      const int64_t s = key < kend ? load_index_dyn(a.slots, a.slots_dtype, key) : 0;
-      const auto p = kbase + s * a.kv_ss;
+      s[st] = slots[key < kend ? key : kend - 1];
+    }
+  };
+  auto load_k = [&](const IdxT (&s)[4], uint4 (&kf)[4][2]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const auto p = kbase + int64_t(s[st]) * a.kv_ss;
       kf[st][0] = gload16(p);
       kf[st][1] = gload16(p + 32);
     }
   };
   const int ntiles = (kend + KT - 1) / KT;
-  uint4 kf[4][2], kn[4][2];
-  if (live_wave) load_k(0, kf);
-  __syncthreads();  // qk cleared
+  uint4 ka[4][2], kb[4][2];
+  IdxT sidx[4];
+  load_idx(0, sidx);
+  if (live_wave) load_k(sidx, ka);
+  if (ntiles > 1) load_idx(KT, sidx);
+  __syncthreads();  // qk and the ring cleared
 
-#pragma unroll 1
-  for (int ti = 0; ti < ntiles; ++ti) {
+  auto tile = [&](int ti, const uint4 (&cur)[4][2], uint4 (&nxt)[4][2]) {
     const int t0 = ti * KT;
     if (live_wave) {
-      if (ti + 1 < ntiles) load_k(t0 + KT, kn);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        landed(cur[st][0]);
+        landed(cur[st][1]);
+      }
+      if (ti + 1 < ntiles) {
+        load_k(sidx, nxt);
+        if (ti + 2 < ntiles) load_idx(t0 + 2 * KT, sidx);
+      }
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         // Neither query of the row-block credits this tile (uniform; past the chunk a limit is 0).
@@ -402,8 +437,8 @@ __global__ __launch_bounds__(pb::THREADS) void prefill_block_kernel(PrefillArgs 
         if (rb_lim <= t0) continue;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-          f32x4_t d = mfma16x16x32(qa[rb][0], as_bf16x8(kf[st][0]), f32x4_t{0.f, 0.f, 0.f, 0.f});
-          d = mfma16x16x32(qa[rb][1], as_bf16x8(kf[st][1]), d);
+          f32x4_t d = mfma16x16x32(qa[rb][0], as_bf16x8(cur[st][0]), f32x4_t{0.f, 0.f, 0.f, 0.f});
+          d = mfma16x16x32(qa[rb][1], as_bf16x8(cur[st][1]), d);
           const float e0 = fast_exp2(fmaf(d[0], a.scale2, -nrm[rb][0]));
           const float e1 = fast_exp2(fmaf(d[1], a.scale2, -nrm[rb][1]));
           const float e2 = fast_exp2(fmaf(d[2], a.scale2, -nrm[rb][2]));
@@ -429,24 +464,29 @@ __global__ __launch_bounds__(pb::THREADS) void prefill_block_kernel(PrefillArgs 
     }
     __syncthreads();
     if (threadIdx.x < KT) {
-      const int key = threadIdx.x;
-      if ((key & ((1 << shift) - 1)) == 0 && t0 + key < kend) {
-        float tot = 0.f;
+      float tot = 0.f;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) tot += part[w][key];
-        if (tot > 0.f) {
-          const int64_t s = load_index_dyn(a.slots, a.slots_dtype, t0 + key);
-          unsafeAtomicAdd(&a.scores[s * a.sss], tot);
-        }
-      }
+      for (int w = 0; w < WAVES; ++w) tot += part[w][threadIdx.x];
+      ring[ti % RING][threadIdx.x] += tot;
     }
-    if (live_wave && ti + 1 < ntiles) {
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        kf[st][0] = kn[st][0];
-        kf[st][1] = kn[st][1];
+    if ((ti + 1) % RING == 0 || ti + 1 == ntiles) {
+      // The ring's credits to the block counters: one atomic per credited block and workgroup.
+      __syncthreads();
+      const int base = (ti - ti % RING) * KT;
+      for (int t = threadIdx.x; t < RING * KT; t += blockDim.x) {
+        const int key = base + t;
+        const float v = ring[t / KT][t % KT];
+        if ((key & ((1 << shift) - 1)) == 0 && key < kend && v > 0.f)
+          unsafeAtomicAdd(&a.scores[int64_t(slots[key]) * a.sss], v);
+        ring[t / KT][t % KT] = 0.f;
       }
+      __syncthreads();
     }
+  };
+#pragma unroll 1
+  for (int ti = 0; ti < ntiles; ti += 2) {
+    tile(ti, ka, kb);
+    if (ti + 1 < ntiles) tile(ti + 1, kb, ka);
   }
 }
 
@@ -698,8 +738,11 @@ extern "C" int gse_prefill_scores(const void* q, int64_t q_stride_t, int64_t q_s
     if (kv_heads > pb::WAVES) return gse_fail(GSE_ESHAPE, "prefill: block counters need kv_heads <= 8");
     hipLaunchKernelGGL((prefill_kernel<1, false>), grid, dim3(64 * pf::waves<1>()), 0, s, a);
     if (int rc = gse_launch_check("prefill pass 1")) return rc;
-    hipLaunchKernelGGL(prefill_block_kernel, dim3(static_cast<uint32_t>((count + pb::QB - 1) / pb::QB)),
-                       dim3(pb::THREADS), 0, s, a);
+    const dim3 bgrid(static_cast<uint32_t>((count + pb::QB - 1) / pb::QB));
+    if (slots_dtype == GSE_I64)
+      hipLaunchKernelGGL(prefill_block_kernel<int64_t>, bgrid, dim3(pb::THREADS), 0, s, a);
+    else
+      hipLaunchKernelGGL(prefill_block_kernel<int32_t>, bgrid, dim3(pb::THREADS), 0, s, a);
     return gse_launch_check("prefill block counters");
   }
   if (kind == 2) {
