@@ -59,6 +59,15 @@ struct FlushArgs {
   float scale2;  // sm_scale * log2(e)
 };
 
+// Column c's slot in the row's list (fill's order: the table's count entries, then req_to_token
+// from the frontier), c clamped to the list's first len entries. The address is selected, not
+// the load, so a batch of these is one round of independent loads.
+GSE_DEVICE int32_t list_slot(const FlushArgs& a, int64_t row, int64_t cnt, int64_t fr, int c, int len) {
+  const int64_t cc = c < len ? c : len - 1;
+  const int32_t* p = cc < cnt ? a.table + row * a.table_stride + cc : a.r2t + row * a.r2t_stride + (fr + cc - cnt);
+  return *p;
+}
+
 // One 64-key tile of a wave: K of keys tb + 16*st + col in registers, then per pair of
 // queued queries eight MFMAs (four 16-key sub-tiles) and the exponentials. Sum mode adds
 // each lane's four heads in-lane and leaves the head/query reduction across lanes to the
@@ -87,14 +96,14 @@ GSE_DEVICE void flush_tile(const FlushArgs& a, const uint16_t* qs, const float* 
   using namespace fl;
   const int lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
+  // The tile's four slot indices in one round of loads, then its K rows in another (a column
+  // past the lists reads the last listed slot and is masked).
   int32_t slot[4];
   uint4 kf[4][2];
 #pragma unroll
+  for (int st = 0; st < 4; ++st) slot[st] = list_slot(a, row, cnt, fr, tb + 16 * st + col, maxlim);
+#pragma unroll
   for (int st = 0; st < 4; ++st) {
-    const int c = tb + 16 * st + col;
-    const int cc = c < maxlim ? c : maxlim - 1;
-    const int32_t s = cc < cnt ? a.table[row * a.table_stride + cc] : a.r2t[row * a.r2t_stride + fr + cc - cnt];
-    slot[st] = c < maxlim ? s : 0;
     const auto p = kp + uint64_t(uint32_t(slot[st])) * uint64_t(a.kv_ss);
     kf[st][0] = gload16(p);
     kf[st][1] = gload16(p + 32);
@@ -290,11 +299,9 @@ __global__ __launch_bounds__(fs::THREADS) void score_flush_short_kernel(FlushArg
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool live = g < a.kv_heads;
   const int64_t cnt = a.count[row], fr = a.frontier[row];
-  auto slot_of = [&](int c) -> int32_t {
-    const int cc = c < maxlim ? c : maxlim - 1;
-    const int32_t s = cc < cnt ? a.table[row * a.table_stride + cc] : a.r2t[row * a.r2t_stride + fr + cc - cnt];
-    return c < maxlim ? s : 0;
-  };
+  // Slot indices stay as loaded until the next chunk turns them into addresses (a column past
+  // the list reads the last listed slot; its K is masked and its score row left alone).
+  auto slot_of = [&](int c) -> int32_t { return list_slot(a, row, cnt, fr, c, maxlim); };
   const uint16_t* qsrc = a.pq + (qbase * a.cap) * a.q_heads * fl::D;
   const float* nsrc = a.pnorm + (qbase * a.cap) * a.q_heads;
   // The queued (query, head) rows of queries [q0, q0 + 8) and their normalisers (log2 units; a
@@ -324,29 +331,44 @@ __global__ __launch_bounds__(fs::THREADS) void score_flush_short_kernel(FlushArg
   const int half = (lane >> 4) & 1;
   const bool updater = lane < 32 && g < SUB;
 
-  int32_t sl[SUB], sl_next[SUB];
-  uint4 kf[SUB][2];
-  f32x4_t old = {0.f, 0.f, 0.f, 0.f}, old_next = {0.f, 0.f, 0.f, 0.f};
-  auto load_rows = [&](const int32_t (&s)[SUB], int c, f32x4_t& o) {
+  // Two register sets alternate between chunks: while chunk i computes from one, chunk i+1's K
+  // rows and old score rows land in the other, and chunk i+2's slot indices in `idx`. The loads
+  // for the next chunks are unconditional (past the list they read the last listed slot), so no
+  // value is copied between sets and nothing waits on a load issued during the chunk.
+  int32_t idx[SUB];
+  uint4 kA[SUB][2], kB[SUB][2];
+  f32x4_t oA = {0.f, 0.f, 0.f, 0.f}, oB = {0.f, 0.f, 0.f, 0.f};
+  int32_t slotA = 0, slotB = 0;  // this lane's score-row slot (key 16*g + col of the chunk)
+  // The score row's slot is picked and its load issued before the K loads: a use placed after a
+  // conditional batch of loads makes the compiler wait for the whole batch.
+  auto load_rows = [&](uint4 (&kf)[SUB][2], f32x4_t& o, int32_t& my_slot) {
+    my_slot = idx[g < SUB ? g : 0];
+    if (rows32 && updater) o = *reinterpret_cast<const f32x4_t*>(sbase + uint64_t(uint32_t(my_slot)) * 8 + 4 * half);
+    if (live) {
 #pragma unroll
-    for (int st = 0; st < SUB; ++st) {
-      if (live) {
-        const auto p = kp + uint64_t(uint32_t(s[st])) * uint64_t(a.kv_ss);
+      for (int st = 0; st < SUB; ++st) {
+        const auto p = kp + uint64_t(uint32_t(idx[st])) * uint64_t(a.kv_ss);
         kf[st][0] = gload16(p);
         kf[st][1] = gload16(p + 32);
       }
     }
-    if (rows32 && updater && c + 16 * g + col < maxlim)
-      o = *reinterpret_cast<const f32x4_t*>(sbase + uint64_t(uint32_t(s[g < SUB ? g : 0])) * 8 + 4 * half);
   };
-  int c0 = blockIdx.x * KEYS;
+  auto load_idx = [&](int c) {
 #pragma unroll
-  for (int st = 0; st < SUB; ++st) sl[st] = slot_of(c0 + 16 * st + col);
-  load_rows(sl, c0, old);
+    for (int st = 0; st < SUB; ++st) idx[st] = slot_of(c + 16 * st + col);
+  };
+  auto chunk = [&](int c0, const uint4 (&kf)[SUB][2], const f32x4_t& old, int32_t my_slot, uint4 (&kn)[SUB][2],
+                   f32x4_t& on, int32_t& sn) {
+    if (live) {
 #pragma unroll
-  for (int st = 0; st < SUB; ++st) sl_next[st] = c0 + stride < maxlim ? slot_of(c0 + stride + 16 * st + col) : 0;
-
-  for (; c0 < maxlim; c0 += stride) {
+      for (int st = 0; st < SUB; ++st) {
+        landed(kf[st][0]);
+        landed(kf[st][1]);
+      }
+    }
+    if (rows32 && updater) landed(old[0]), landed(old[1]), landed(old[2]), landed(old[3]);
+    load_rows(kn, on, sn);  // chunk c0 + stride
+    load_idx(c0 + 2 * stride);
     float acc[SUB];
 #pragma unroll
     for (int st = 0; st < SUB; ++st) acc[st] = 0.f;
@@ -373,17 +395,6 @@ __global__ __launch_bounds__(fs::THREADS) void score_flush_short_kernel(FlushArg
         if (grp == 0) red[g][16 * st + col] = tot;
       }
     }
-    // The next chunk's rows go out now (K is free once the MFMAs have read it).
-    const int c1 = c0 + stride;
-    const int32_t my_slot = sl[g < SUB ? g : 0];
-    if (c1 < maxlim) {
-      load_rows(sl_next, c1, old_next);
-#pragma unroll
-      for (int st = 0; st < SUB; ++st) {
-        sl[st] = sl_next[st];
-        sl_next[st] = c1 + stride < maxlim ? slot_of(c1 + stride + 16 * st + col) : 0;
-      }
-    }
     __syncthreads();  // every head's totals of this chunk in LDS
     const int key = 16 * g + col;
     if (updater && c0 + key < maxlim) {
@@ -397,7 +408,14 @@ __global__ __launch_bounds__(fs::THREADS) void score_flush_short_kernel(FlushArg
         for (int h = 0; h < a.kv_heads; ++h) p[h * a.ssg] += red[h][key];
       }
     }
-    old = old_next;
+  };
+  int c0 = blockIdx.x * KEYS;
+  load_idx(c0);
+  load_rows(kA, oA, slotA);
+  load_idx(c0 + stride);
+  for (; c0 < maxlim; c0 += 2 * stride) {
+    chunk(c0, kA, oA, slotA, kB, oB, slotB);
+    if (c0 + stride < maxlim) chunk(c0 + stride, kB, oB, slotB, kA, oA, slotA);
   }
 }
 
@@ -446,17 +464,16 @@ __global__ __launch_bounds__(flb::THREADS) void score_flush_block_kernel(FlushAr
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t cnt = a.count[row], fr = a.frontier[row];
-  auto slot_of = [&](int c) -> int32_t {
-    const int cc = c < maxlim ? c : maxlim - 1;
-    const int32_t s = cc < cnt ? a.table[row * a.table_stride + cc] : a.r2t[row * a.r2t_stride + fr + cc - cnt];
-    return c < maxlim ? s : 0;
-  };
+  auto slot_of = [&](int c) -> int32_t { return list_slot(a, row, cnt, fr, c, maxlim); };
   if (g < a.kv_heads) {
     const auto kp = as_global(static_cast<const uint16_t*>(a.k_pools[l])) + int64_t(g) * a.kv_sh + 8 * grp;
     uint4 kf[SUB][2];
+    int32_t slot[SUB];
+#pragma unroll
+    for (int st = 0; st < SUB; ++st) slot[st] = slot_of(c0 + 16 * st + col);
 #pragma unroll
     for (int st = 0; st < SUB; ++st) {
-      const auto p = kp + uint64_t(uint32_t(slot_of(c0 + 16 * st + col))) * uint64_t(a.kv_ss);
+      const auto p = kp + uint64_t(uint32_t(slot[st])) * uint64_t(a.kv_ss);
       kf[st][0] = gload16(p);
       kf[st][1] = gload16(p + 32);
     }
