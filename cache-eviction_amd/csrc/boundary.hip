@@ -1386,14 +1386,14 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
     const float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
-      kd[r] = gload16(K + int64_t(src[r]) * a.kv_ss + off);
+      kd[r] = gload16_nt(K + int64_t(src[r]) * a.kv_ss + off);
       sc[r] = srow[int64_t(src[r]) * a.sss];
     }
   };
   auto load_v = [&](int l) {
     auto V = as_global(static_cast<const uint16_t*>(pools[1][l]));
 #pragma unroll
-    for (int r = 0; r < PER; ++r) vd[r] = gload16(V + int64_t(src[r]) * a.kv_ss + off);
+    for (int r = 0; r < PER; ++r) vd[r] = gload16_nt(V + int64_t(src[r]) * a.kv_ss + off);
   };
   bool gave_up = false;
   sources(0);
@@ -1417,7 +1417,7 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
       float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
 #pragma unroll
       for (int r = 0; r < PER; ++r) {
-        gstore16(K + int64_t(dst[r]) * a.kv_ss + off, kd[r]);
+        gstore16_nt(K + int64_t(dst[r]) * a.kv_ss + off, kd[r]);
         srow[int64_t(dst[r]) * a.sss] = sc[r];
       }
     }
@@ -1430,7 +1430,7 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
     {
       auto V = as_global(pools[1][l]);
 #pragma unroll
-      for (int r = 0; r < PER; ++r) gstore16(V + int64_t(dst[r]) * a.kv_ss + off, vd[r]);
+      for (int r = 0; r < PER; ++r) gstore16_nt(V + int64_t(dst[r]) * a.kv_ss + off, vd[r]);
     }
   }
 }

@@ -102,6 +102,15 @@ GSE_DEVICE void gstore16(__attribute__((address_space(1))) void* p, uint4 v) {
   *(__attribute__((address_space(1))) u32x4_t*)p = __builtin_bit_cast(u32x4_t, v);
 }
 
+// Streaming forms (nontemporal: the line is not kept in the caches) for data that one kernel
+// touches exactly once, such as rows that a relocation moves.
+GSE_DEVICE uint4 gload16_nt(const __attribute__((address_space(1))) void* p) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t*)p));
+}
+GSE_DEVICE void gstore16_nt(__attribute__((address_space(1))) void* p, uint4 v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), (__attribute__((address_space(1))) u32x4_t*)p);
+}
+
 template <typename T>
 GSE_DEVICE int64_t load_index(const void* p, int64_t i) {
   return int64_t(static_cast<const T*>(p)[i]);
