@@ -29,6 +29,11 @@ constexpr int FUSED_THREADS = 64 * MAX_KVH;
 
 GSE_DEVICE uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// Raw buffer resources (stride 0, word 3 of the descriptor as gfx9-family parts take it): an
+// access whose offset is at or past num_records is dropped by the hardware's range check.
+constexpr int BUFFER_RSRC_FLAGS = 0x00020000;
+constexpr int BUFFER_OUT_OF_RANGE = int(0x80000000u);
+
 
 // Keys per workgroup for P workgroups over T keys (0 when T == 0).
 GSE_DEVICE int fused_chunk(int T, int P) { return (T + P - 1) / P; }
@@ -57,6 +62,13 @@ struct FusedArgs {
   float* part;  // [P + bs, q_heads, PART]
   int bs, q_heads, kv_heads;
   float scale2;  // sm_scale * log2(e)
+  // Kept logits (optional): for a sequence whose row r has 0 <= lidx[r] < lrows, the raw q.k of
+  // list entry c < lcap, head h = 8 * g + j goes to logits[((lidx[r] * kv_heads + g) * lcap + c) * 8 + j].
+  float* logits;
+  const int32_t* lidx;
+  const void* rows;
+  int rows_dtype;
+  int lrows, lcap;
 };
 
 // Per 64-key tile a wave (one KV head) computes S^T = K . Q^T with
@@ -65,7 +77,7 @@ struct FusedArgs {
 // rescale, and O^T += V^T . P^T with V transposed through LDS
 // (ds_read_b64_tr_b16). Slot indices two tiles ahead and K/V rows one tile ahead
 // are issued, unconditionally, before each tile's compute.
-template <typename IdxT>
+template <typename IdxT, bool KEEP>
 __global__ __launch_bounds__(FUSED_THREADS) void decode_fused_kernel(FusedArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vtile[MAX_KVH][TILE * LDS_ROW];
 
@@ -110,6 +122,24 @@ __global__ __launch_bounds__(FUSED_THREADS) void decode_fused_kernel(FusedArgs a
       qf0 = as_bf16x8(ld16(qp));
       qf1 = as_bf16x8(ld16(qp + 32));
     }
+    // This segment's kept logits: the wave's 8 heads of list entry c at lg + c * q_heads.
+    // (KEEP only) A buffer resource over the wave's KV-head plane of the sequence's kept rows,
+    // entries [0, lend): stores past it (lanes of groups 2/3, entries past lend, every entry when
+    // lend = 0) are dropped by the buffer range check, so no store needs a branch.
+    const int seq0 = a.indptr[b];
+    __amdgpu_buffer_rsrc_t lrsrc = __builtin_amdgcn_make_buffer_rsrc(a.logits, 0, 0, BUFFER_RSRC_FLAGS);
+    if (KEEP) {
+      const int kept = __builtin_amdgcn_readfirstlane(a.lidx[load_index_dyn(a.rows, a.rows_dtype, b)]);
+      const bool on = kept >= 0 && kept < a.lrows;
+      const int lend = on ? (s1 - seq0 < a.lcap ? s1 - seq0 : a.lcap) : 0;
+      // Uniform by construction; readfirstlane lets the compiler keep the descriptor in scalar
+      // registers (it cannot prove the CSR bounds uniform).
+      const uint64_t base = uint64_t(a.logits + (on ? (int64_t(kept) * a.q_heads + g * GROUP) * a.lcap : 0));
+      const uint64_t sbase = uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(base)))) |
+                             uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(base >> 32)))) << 32;
+      lrsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(sbase), 0,
+                                                __builtin_amdgcn_readfirstlane(lend * GROUP * 4), BUFFER_RSRC_FLAGS);
+    }
     float m_run = -INFINITY, l_run = 0.f;
     f32x4_t oacc[4];
 #pragma unroll
@@ -146,6 +176,21 @@ __global__ __launch_bounds__(FUSED_THREADS) void decode_fused_kernel(FusedArgs a
         f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
         acc = mfma16x16x32(as_bf16x8(X.k[st][0]), qf0, acc);
         sc[st] = mfma16x16x32(as_bf16x8(X.k[st][1]), qf1, acc);
+      }
+      if (KEEP) {
+        // Kept logits: Q . K^T with the operands swapped, so a lane of groups 0/1 holds heads
+        // 4*grp..4*grp+3 of key 16*st + col (the products the score flush forms from the queued
+        // query) and stores them as one 16-byte piece of the key's 32-byte row in the wave's
+        // KV-head plane: a store instruction writes 512 contiguous bytes. Every lane issues its
+        // store (out of range where nothing is kept), so the compiler's load waits stay exact.
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          f32x4_t d = mfma16x16x32(qf0, as_bf16x8(X.k[st][0]), f32x4_t{0.f, 0.f, 0.f, 0.f});
+          d = mfma16x16x32(qf1, as_bf16x8(X.k[st][1]), d);
+          const int c = tb - seq0 + 16 * st + col;
+          const int off = grp < 2 ? (c * GROUP + 4 * grp) * 4 : BUFFER_OUT_OF_RANGE;
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, d), lrsrc, off, 0, 0);
+        }
       }
       if (tb + TILE > s1) {  // the segment's last tile: keys past its end take no mass
         const int lim = s1 - tb;
@@ -615,7 +660,8 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
                           void* queue_q, float* queue_norm, int32_t* queue_lim, int32_t* queue_count, int queue_cap,
                           int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int max_len,
-                          int score_mode, void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
+                          int score_mode, float* logits, const int32_t* logit_index, int logit_rows, int logit_cap,
+                          void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
   if (int rc = check_decode_shape(q_heads, kv_heads, head_dim)) return rc;
   if (bs < 0) return gse_fail(GSE_EINVAL, "decode: bs < 0");
   if (bs == 0) return GSE_OK;
@@ -629,6 +675,10 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   if (score_mode == GSE_SCORE_EAGER && !scores) return gse_fail(GSE_EINVAL, "decode: eager scoring needs scores");
   if (score_mode == GSE_SCORE_QUEUE && (!queue_q || !queue_norm || !queue_lim || !queue_count || queue_cap < 1))
     return gse_fail(GSE_EINVAL, "decode: queue mode needs the queue buffers and queue_cap >= 1");
+  if (logits && (!logit_index || !rows || logit_rows < 1 || logit_cap < 1))
+    return gse_fail(GSE_EINVAL, "decode: kept logits need logit_index, rows, logit_rows >= 1 and logit_cap >= 1");
+  if (logits && int64_t(logit_cap) * q_heads * 4 >= (int64_t(1) << 31))
+    return gse_fail(GSE_EINVAL, "decode: kept logits of one row must stay below 2 GiB");
   if ((q_stride_h % 8) || (q_stride_b % 8) || (kv_stride_s % 8) || (kv_stride_h % 8) || (o_stride_b % 8) ||
       (o_stride_h % 8))
     return gse_fail(GSE_EINVAL, "decode: strides must be multiples of 8 elements (16-byte rows)");
@@ -654,11 +704,24 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   f.q_heads = q_heads;
   f.kv_heads = kv_heads;
   f.scale2 = sm_scale * kLog2e;
+  if (logits) {
+    f.logits = logits;
+    f.lidx = logit_index;
+    f.rows = rows;
+    f.rows_dtype = rows_dtype;
+    f.lrows = logit_rows;
+    f.lcap = logit_cap;
+  }
   const dim3 grid(P), block(FUSED_THREADS);
-  if (indices_dtype == GSE_I64)
-    hipLaunchKernelGGL(decode_fused_kernel<int64_t>, grid, block, 0, s, f);
+  // Kept logits take the kernel instance that has their MFMAs and stores; the other has none.
+  if (indices_dtype == GSE_I64 && logits)
+    hipLaunchKernelGGL((decode_fused_kernel<int64_t, true>), grid, block, 0, s, f);
+  else if (indices_dtype == GSE_I64)
+    hipLaunchKernelGGL((decode_fused_kernel<int64_t, false>), grid, block, 0, s, f);
+  else if (logits)
+    hipLaunchKernelGGL((decode_fused_kernel<int32_t, true>), grid, block, 0, s, f);
   else
-    hipLaunchKernelGGL(decode_fused_kernel<int32_t>, grid, block, 0, s, f);
+    hipLaunchKernelGGL((decode_fused_kernel<int32_t, false>), grid, block, 0, s, f);
   int rc = gse_launch_check("decode_fused");
   if (rc) return rc;
 

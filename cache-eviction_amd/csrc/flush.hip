@@ -527,6 +527,84 @@ __global__ __launch_bounds__(flb::THREADS) void score_flush_block_kernel(FlushAr
   }
 }
 
+// One-step queues whose products the decode kernel kept. Grid (ceil(max_len / lf::KEYS), n_rows,
+// layers), 256 threads: lane (key k = lane / 8, KV head g = lane % 8) of wave w takes list
+// entries c = c0 + 32 * u + 8 * w + k, u < 4, reads the 8 products of its head group (two
+// 16-byte loads of the entry's 8-float row in the KV head's plane), and adds
+//   sum (kind 1) or max (kind 2) over the group's heads h of exp2(p_h * scale2 - norm_h)
+// to the entry's score in head g (norm_h in log2 units): the terms and the order of the additions of
+// score_flush_short_kernel for a queue of one step, so the two agree bit for bit. The slot
+// indices are loaded first, then the products, then the old scores (whose wait leaves the
+// products in flight).
+namespace lf {
+constexpr int THREADS = 256;
+constexpr int UNROLL = 4;
+constexpr int KEYS = UNROLL * (THREADS / 8);  // list entries per workgroup
+}  // namespace lf
+
+struct LogitArgs {
+  const float* logits;
+  int64_t layer_stride;
+  const int32_t* lidx;
+  int lrows, lcap;
+};
+
+__global__ __launch_bounds__(lf::THREADS) void score_flush_logits_kernel(FlushArgs a, LogitArgs la) {
+  using namespace lf;
+  const int l = blockIdx.z;
+  const int64_t row = load_index_dyn(a.rows, a.rows_dtype, blockIdx.y);
+  const int word = a.mode[row];
+  const int md = score_kind(word);
+  if (md != 1 && md != 2) return;
+  const int64_t qbase = int64_t(l) * a.rows_total + row;
+  if (a.pcount[qbase] != 1) return;
+  const int kept = la.lidx[row];
+  if (kept < 0 || kept >= la.lrows) return;
+  int lim = a.plim[qbase * a.cap] - score_delay(word);
+  lim = lim < la.lcap ? lim : la.lcap;
+  const int c0 = blockIdx.x * KEYS;
+  if (c0 >= lim) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int g = lane & 7, k = lane >> 3;
+  if (g >= a.kv_heads) return;
+  const float* lrow = la.logits + l * la.layer_stride + (int64_t(kept) * a.q_heads + 8 * g) * la.lcap;
+  const float* nrm = a.pnorm + qbase * a.cap * a.q_heads + 8 * g;
+  float* srow = a.scores + l * a.ssl + g * a.ssg;
+  const int64_t cnt = a.count[row], fr = a.frontier[row];
+  int c[UNROLL];
+  int32_t slot[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    c[u] = c0 + 32 * u + 8 * w + k;
+    slot[u] = list_slot(a, row, cnt, fr, c[u], lim);
+  }
+  // Normalisers are queued as natural logs; log2 units as the short flush stages them.
+  const f32x4_t n0 = *reinterpret_cast<const f32x4_t*>(nrm) * kLog2e;
+  const f32x4_t n1 = *reinterpret_cast<const f32x4_t*>(nrm + 4) * kLog2e;
+  f32x4_t p0[UNROLL], p1[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const float* p = lrow + int64_t(c[u] < lim ? c[u] : lim - 1) * 8;
+    p0[u] = *reinterpret_cast<const f32x4_t*>(p);
+    p1[u] = *reinterpret_cast<const f32x4_t*>(p + 4);
+  }
+  float old[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) old[u] = srow[int64_t(uint32_t(slot[u])) * a.sss];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    float e[8];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      e[h] = fast_exp2(fmaf(p0[u][h], a.scale2, -n0[h]));
+      e[4 + h] = fast_exp2(fmaf(p1[u][h], a.scale2, -n1[h]));
+    }
+    const float tot = md == 2 ? fmaxf(fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3])), fmaxf(fmaxf(e[4], e[5]), fmaxf(e[6], e[7])))
+                              : ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+    if (c[u] < lim) srow[int64_t(uint32_t(slot[u])) * a.sss] = old[u] + tot;
+  }
+}
+
 // The queues of the flushed (layer, row) pairs are empty afterwards; a count above the
 // capacity (steps the decode merge could not queue) sets *overflow.
 __global__ void flush_clear_kernel(const void* rows, int rows_dtype, int n_rows, int layers, int rows_total, int cap,
@@ -663,6 +741,40 @@ extern "C" int gse_score_flush_blocks(void* const* k_pools, int layers, int64_t 
     hipLaunchKernelGGL(score_flush_block_kernel, dim3(chunks, unsigned(n_rows), unsigned(layers)), dim3(flb::THREADS),
                        0, s, f);
     if (int rc = gse_launch_check("score_flush_blocks")) return rc;
+  }
+  return flush_clear(f, n_rows, overflow, s);
+}
+
+extern "C" int gse_score_flush_logits(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                                      float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                                      int64_t scores_stride_s, const int32_t* table, int64_t table_stride,
+                                      const int32_t* req_to_token, int64_t r2t_stride, const int32_t* frontier,
+                                      const int32_t* count, const int32_t* mode_by_row, const void* rows,
+                                      int rows_dtype, int n_rows, int64_t max_len, const void* pend_q,
+                                      const float* pend_norm, const int32_t* pend_lim, int32_t* pend_count,
+                                      int rows_total, int queue_cap, int q_heads, int kv_heads, int head_dim,
+                                      float sm_scale, const float* logits, int64_t logits_layer_stride,
+                                      const int32_t* logit_index, int logit_rows, int logit_cap, int32_t* overflow,
+                                      gse_stream_t stream) {
+  FlushArgs f = {};
+  if (int rc = flush_args(f, k_pools, layers, kv_stride_s, kv_stride_h, scores, scores_stride_l, scores_stride_g,
+                          scores_stride_s, table, table_stride, req_to_token, r2t_stride, frontier, count,
+                          mode_by_row, rows, rows_dtype, n_rows, max_len, pend_q, pend_norm, pend_lim, pend_count,
+                          rows_total, queue_cap, q_heads, kv_heads, head_dim, sm_scale))
+    return rc;
+  if (n_rows == 0 || layers == 0) return GSE_OK;
+  if (!logits || !logit_index || logit_rows < 1 || logit_cap < 1 || logits_layer_stride < 0)
+    return gse_fail(GSE_EINVAL, "score_flush_logits: need logits, logit_index, logit_rows >= 1 and logit_cap >= 1");
+  if (logits_layer_stride > 0 && logits_layer_stride < int64_t(logit_rows) * logit_cap * q_heads)
+    return gse_fail(GSE_EINVAL, "score_flush_logits: layers' logits overlap");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t len = max_len < logit_cap ? max_len : logit_cap;
+  const unsigned chunks = unsigned((len + lf::KEYS - 1) / lf::KEYS);
+  if (chunks) {
+    const LogitArgs la = {logits, logits_layer_stride, logit_index, logit_rows, logit_cap};
+    hipLaunchKernelGGL(score_flush_logits_kernel, dim3(chunks, unsigned(n_rows), unsigned(layers)),
+                       dim3(lf::THREADS), 0, s, f, la);
+    if (int rc = gse_launch_check("score_flush_logits")) return rc;
   }
   return flush_clear(f, n_rows, overflow, s);
 }

@@ -48,13 +48,15 @@ SIGNATURES = {
     "gse_zero_slots": (_i, [_p, _i, _l, _i, _l, _l, _p, _i, _l, _p]),
     "gse_decode_workspace_bytes": (_l, [_i, _i, _i]),
     "gse_decode": (_i, [_p, _l, _l, _p, _p, _l, _l, _p, _p, _i, _p, _i, _p, _p, _i, _p, _l, _l, _p, _l, _l, _p,
-                        _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _i, _i, _p, _l, _p]),
+                        _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _i, _i, _p, _p, _i, _i, _p, _l, _p]),
     "gse_score_flush": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p, _p,
                              _p, _p, _i, _i, _i, _i, _i, _f, _p, _p]),
     "gse_score_flush_short": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p,
                                    _p, _p, _p, _i, _i, _i, _i, _i, _f, _p, _p]),
     "gse_score_flush_blocks": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p,
                                     _p, _p, _p, _i, _i, _i, _i, _i, _f, _p, _p]),
+    "gse_score_flush_logits": (_i, [_p, _i, _l, _l, _p, _l, _l, _l, _p, _l, _p, _l, _p, _p, _p, _p, _i, _i, _l, _p,
+                                    _p, _p, _p, _i, _i, _i, _i, _i, _f, _p, _l, _p, _i, _i, _p, _p]),
     "gse_decode_scores_from_lse": (_i, [_p, _l, _l, _p, _l, _l, _p, _p, _i, _p, _l, _l, _p, _i, _i, _p, _i,
                                         _p, _p, _i, _p, _l, _l, _i, _i, _i, _i, _f, _i, _p, _l, _p]),
     "gse_reservoir_scores": (_i, [_p, _i, _p, _p, _i, _i, _l, _l, _p, _p]),

@@ -47,6 +47,15 @@ class State:
         self.qq = self.qnorm = self.qlim = None
         self.qcount = torch.zeros((len(self.full_layers), n_rows), **i32)
         self.queued = {}
+        # Kept decode products (gse_score_flush_logits): row -> index in the logits buffer on the
+        # device (logit_index), the rows whose products of the current step are still unfolded,
+        # the full-layer indices decoded with products kept this step, and (rows, cap) of the
+        # buffer's layout.
+        self.logit_index = None
+        self.logit_rows_on_device = {}
+        self.logit_fresh = set()
+        self.logit_layers = set()
+        self.logit_layout = (0, 0)
         self.row_ids = torch.arange(n_rows, **i32)
         self.layer_scaling = {}  # full-layer index -> softmax scale of its queued queries
         self._ws = {}
@@ -96,7 +105,7 @@ class State:
 
     def _pin_rows(self):
         if self._rows_host is None:
-            total = self.req_to_token.shape[0]
+            total = 3 * self.req_to_token.shape[0]  # room for two row lists and one value list
             self._rows_host = torch.zeros(total, dtype=torch.int32, pin_memory=True)
             self._rows_dev = torch.zeros(total, dtype=torch.int32, device=self.device)
             self._rows_copied = torch.cuda.Event()
@@ -117,6 +126,7 @@ class State:
         self.qq = torch.zeros((layers, n_rows, cap, self.q_heads, self.dim), dtype=torch.bfloat16, device=self.device)
         self.qnorm = torch.zeros((layers, n_rows, cap, self.q_heads), dtype=torch.float32, device=self.device)
         self.qlim = torch.zeros((layers, n_rows, cap), dtype=torch.int32, device=self.device)
+        self.logit_index = torch.full((n_rows,), -1, dtype=torch.int32, device=self.device)
         # Pinned host buffers now, at the first decode step: allocating pinned memory
         # synchronises the device, which would drain the GPU if done mid-run.
         self.status_block()
@@ -146,3 +156,4 @@ class State:
             t[row] = 0
         self.qcount[:, row] = 0
         self.queued.pop(row, None)
+        self.logit_fresh.discard(row)

@@ -170,6 +170,12 @@ int64_t gse_decode_workspace_bytes(int bs, int q_heads, int head_dim);
  * the batch's keys; fixed grid, no host reads: capturable in a HIP graph. rows[b] must
  * index mode_by_row and the queue buffers (as SGLang's req_pool_indices index
  * req_to_token): the kernels do not check it.
+ * Kept logits (logits may be null): for a sequence whose row has
+ *   k = logit_index[rows[b]] in [0, logit_rows), the fp32 products q_h.k_c (unscaled) of its
+ *   list entries c < min(list length, logit_cap) are written to logits[((k * kv_heads + g) *
+ *   logit_cap + c) * 8 + j] for query head h = 8 * g + j (a plane per KV head);
+ *   gse_score_flush_logits then adds a one-step queue's scores from them instead of reading K
+ *   again. Entries of other sequences, and c >= logit_cap, are not written.
  */
 int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
@@ -179,7 +185,8 @@ int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
                void* queue_q, float* queue_norm, int32_t* queue_lim, int32_t* queue_count, int queue_cap,
                int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int max_len,
-               int score_mode, void* workspace, int64_t workspace_bytes, gse_stream_t stream);
+               int score_mode, float* logits, const int32_t* logit_index, int logit_rows, int logit_cap,
+               void* workspace, int64_t workspace_bytes, gse_stream_t stream);
 
 /*
  * score_flush — add the queued decode scores of the listed rows, for every full
@@ -238,6 +245,28 @@ int gse_score_flush_blocks(void* const* k_pools, int layers, int64_t kv_stride_s
                            const int32_t* queue_lim, int32_t* queue_count, int rows_total, int queue_cap,
                            int q_heads, int kv_heads, int head_dim, float sm_scale, int32_t* overflow,
                            gse_stream_t stream);
+
+/*
+ * score_flush_logits — gse_score_flush for rows whose queue holds exactly one step whose
+ * products gse_decode kept (rows that evict at every step): same arguments and result, with
+ * q_h.k_c read from `logits` (layer l's at logits + l * logits_layer_stride floats, laid out as
+ * gse_decode writes them; logit_index, logit_rows and logit_cap as given to it) instead of
+ * recomputed from K, 256 bytes per list entry read instead of 1024. K is not read. Rows of
+ * score kinds 1 and 2 whose queue count is 1 and whose logit_index is in range are folded, for
+ * entries c < min(lim - delay, logit_cap); the queues of every listed row are emptied. For
+ * such a row the scores equal gse_score_flush_short's bit for bit. No reference counterpart
+ * (R:189-200 adds each step eagerly).
+ */
+int gse_score_flush_logits(void* const* k_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,
+                           float* scores, int64_t scores_stride_l, int64_t scores_stride_g,
+                           int64_t scores_stride_s, const int32_t* table, int64_t table_stride,
+                           const int32_t* req_to_token, int64_t r2t_stride, const int32_t* frontier,
+                           const int32_t* count, const int32_t* mode_by_row, const void* rows, int rows_dtype,
+                           int n_rows, int64_t max_len, const void* queue_q, const float* queue_norm,
+                           const int32_t* queue_lim, int32_t* queue_count, int rows_total, int queue_cap,
+                           int q_heads, int kv_heads, int head_dim, float sm_scale, const float* logits,
+                           int64_t logits_layer_stride, const int32_t* logit_index, int logit_rows, int logit_cap,
+                           int32_t* overflow, gse_stream_t stream);
 
 /*
  * decode_scores_from_lse —the reference's score update given an external

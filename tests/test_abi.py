@@ -58,7 +58,7 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
         pytest.skip("library not built")
     lib = _native.lib()
     rc = lib.gse_decode(None, 0, 0, None, None, 0, 0, None, None, 0, None, 0, None, None, 0, None, 0, 1, None, 0, 0,
-                        None, None, None, None, None, 0, 4, 64, 8, 128, 0.125, 512, 0, None, 0, None)
+                        None, None, None, None, None, 0, 4, 64, 8, 128, 0.125, 512, 0, None, None, 0, 0, None, 0, None)
     assert rc != 0 and b"head_dim" in lib.gse_last_error()
     rc = lib.gse_fill(None, 0, None, 0, None, 0, None, 0, None, None, -1, 0, None, None, 0, None)
     assert rc != 0
@@ -103,6 +103,25 @@ def test_block_flush_rejects_bad_arguments_without_a_gpu():
     rc = lib.gse_prefill_scores(None, 0, 0, 10, None, 0, 0, None, 0, 10, 0, None, 0, 1 | 2 << 4, None, 0, 0, 64, 8,
                                 64, 0.125, None, 0, None)
     assert rc != 0 and b"block size" in lib.gse_last_error()
+
+
+def test_logit_flush_rejects_bad_arguments_without_a_gpu():
+    """Host-side checks of gse_score_flush_logits and of gse_decode's kept-logit arguments (the
+    pointers are host buffers: validation fails before any launch)."""
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    import ctypes
+    lib = _native.lib()
+    buf = ctypes.create_string_buffer(256)
+    p = ctypes.addressof(buf)
+    args = [p, 12, 512, 64, p, 0, 0, 0, p, 0, p, 0, p, p, p, p, 0, 1, 100, p, p, p, p, 4, 64, 64, 8, 64, 0.125]
+    rc = lib.gse_score_flush_logits(*args, None, 0, p, 1, 100, None, None)
+    assert rc != 0 and b"logits" in lib.gse_last_error()
+    rc = lib.gse_score_flush_logits(*args, p, 10, p, 1, 100, None, None)
+    assert rc != 0 and b"overlap" in lib.gse_last_error()
+    rc = lib.gse_decode(p, 0, 0, p, p, 0, 0, p, p, 0, p, 0, p, p, 0, None, 0, 1, p, 0, 0, None, p, p, p, p, 4, 4, 64,
+                        8, 64, 0.125, 512, 2, p, None, 1, 10, p, 1 << 30, None)
+    assert rc != 0 and b"kept logits" in lib.gse_last_error()
 
 
 def test_row_descriptors_match_the_header_layout(tmp_path):
