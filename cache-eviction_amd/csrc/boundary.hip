@@ -629,26 +629,26 @@ GSE_DEVICE int cmp96(uint32_t hi, uint32_t lo, uint32_t pos, uint32_t th, uint32
   return cmp_top(pos, tp, fixed - 8);
 }
 
-// Sets bit p of the LDS bitmap for the lanes with `act`. Lanes whose positions share a 32-bit
-// word pool their bits first (positions of neighbouring columns mostly do): up to 4 rounds, each
-// taking the lowest active lane's word, one atomic per round; lanes left after that OR alone.
+// Sets bit p of the LDS bitmap for the lanes with `act` (the whole wave calls it).
 GSE_DEVICE void wave_set_bit(uint32_t* words, int32_t p, bool act) {
-  const uint32_t w = uint32_t(p) >> 5, bit = 1u << (uint32_t(p) & 31u);
+  // A segmented OR over lanes: each lane gathers the bits of later lanes that fall in its word
+  // (doubling steps, joining a lane o places on only when it holds the same word), and the first
+  // lane of each run of equal words adds the run's bits with one atomic. Lanes of one run are
+  // never missed; a later run of the same word adds its bits again, which OR absorbs. Columns in
+  // position order (the common case) give one atomic per touched word.
   const int lane = threadIdx.x & 63;
+  const int32_t w = act ? int32_t(uint32_t(p) >> 5) : -1;
+  uint32_t v = act ? 1u << (uint32_t(p) & 31u) : 0u;
 #pragma unroll
-  for (int round = 0; round < 4; ++round) {
-    const uint64_t live = __ballot(act);
-    if (!live) return;
-    const int leader = __ffsll(static_cast<unsigned long long>(live)) - 1;
-    const uint32_t lw = __shfl(w, leader, 64);
-    const bool mine = act && w == lw;
-    uint32_t v = mine ? bit : 0u;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) v |= __shfl_xor(v, o, 64);
-    if (lane == leader) atomicOr(&words[lw], v);
-    act = act && !mine;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_down(v, o, 64);
+    const int32_t wy = __shfl_down(w, o, 64);
+    if (lane + o < 64 && wy == w) v |= y;
   }
-  if (act) atomicOr(&words[w], bit);
+  const int32_t wprev = __shfl_up(w, 1, 64);
+  if (act && (lane == 0 || wprev != w)) atomicOr(&words[w], v);
+  // One column at a time: interleaving the scans of a batch of columns only adds live registers.
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // wpre[w] = set bits of words[0, w) (one block scan over contiguous runs of words); the rank
@@ -928,6 +928,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
   int* wpre = reinterpret_cast<int*>(keys + a.nwords);
   for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
   __syncthreads();
+#pragma unroll 1
   for (int k0 = 0; k0 < KPT; k0 += BATCH) {
     int32_t pb[BATCH];
     load_pos(k0, pb);
@@ -939,6 +940,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
   }
   __syncthreads();
   bitmap_word_prefix(words, a.nwords, wpre, tmp);
+#pragma unroll 1
   for (int k0 = 0; k0 < KPT; k0 += BATCH) {
     int32_t pb[BATCH];
     load_pos(k0, pb);
