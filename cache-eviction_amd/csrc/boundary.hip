@@ -89,6 +89,28 @@ GSE_DEVICE int block_exclusive_scan(int v, int* tmp, int* total) {
   return before + x - v;
 }
 
+// Ordered compaction by waves: wave w owns the contiguous index range [w * span, (w + 1) * span)
+// of [0, n), span = ceil(n / waves) rounded up to 64. Given each wave's count of kept indices
+// (lane 0 of each wave passes it), returns in every lane of wave w the number kept before its
+// range (exclusive scan over the waves through LDS `tmp`, at least 16 ints). Synchronises the
+// workgroup.
+GSE_DEVICE int wave_range_offset(int wave_count, int* tmp) {
+  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) tmp[wave] = wave_count;
+  __syncthreads();
+  int off = 0;
+  for (int w = 0; w < wave; ++w) off += tmp[w];
+  __syncthreads();
+  (void)nw;
+  return off;
+}
+
+// 64-bit mask of the lanes below this one.
+GSE_DEVICE uint64_t lanes_below() {
+  const int lane = threadIdx.x & 63;
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
 GSE_DEVICE int block_sum(int v, int* tmp) {
   int total;
   block_exclusive_scan<SEL_THREADS>(v, tmp, &total);
@@ -965,6 +987,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
 // more than 32 atomics per barrier (with all 256 workgroups on one counter the relocation ran at
 // 1.3 TB/s). Polls sleep 20 x 64 cycles between reads.
 constexpr int COOP_THREADS = 1024;
+constexpr int COOP_WAVES_SEL = SEL_THREADS / 64;  // waves of a SEL_THREADS workgroup
 constexpr int COOP_WAVES = COOP_THREADS / 64;
 constexpr int COOP_SLEEP = 20;
 constexpr int COOP_SPIN_LIMIT = 1 << 18;
@@ -1057,44 +1080,32 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndBatch b) {
   }
   __syncthreads();
   int32_t* trow = a.table + int64_t(a.row) * a.table_stride;
-  // Unprotected columns in column order, 32 per thread per pass: target j = rank j < width
-  // (also the table's column Q + j), leftover beyond.
-  int carry = 0;
-  for (int base = 0; base < a.nwords_cols; base += SEL_THREADS) {
-    const int w = base + threadIdx.x;
-    const int64_t lo = int64_t(w) << 5;
-    uint32_t bits = 0;
-    if (w < a.nwords_cols) {
-      const uint32_t valid = lo + 32 <= a.N ? 0xffffffffu : ((1u << (a.N - lo)) - 1u);
-      bits = ~words[w] & valid;
-    }
-    int total;
-    const int ex = block_exclusive_scan<SEL_THREADS>(__popc(bits), tmp, &total);
-    int j = carry + ex;
-    // The word's 32 slots are loaded together (slots has room for whole words), then stored.
-    int32_t sl[32];
-    if (bits) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int4 v = *reinterpret_cast<const int4*>(a.slots + lo + 4 * q);
-        sl[4 * q] = v.x;
-        sl[4 * q + 1] = v.y;
-        sl[4 * q + 2] = v.z;
-        sl[4 * q + 3] = v.w;
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < 32; ++t) {
-      if (!(bits >> t & 1u)) continue;
-      if (j < width) {
-        a.targets[j] = sl[t];
-        trow[Q + j] = sl[t];
+  // Unprotected columns in column order: target j = rank j < width (also the table's column
+  // Q + j), leftover beyond. Wave w ranks the columns of its contiguous range, 64 at a time with
+  // a ballot (one column per lane: the slot loads and the stores are contiguous), after the
+  // counts of the ranges before it.
+  const int lane = threadIdx.x & 63;
+  const int64_t span = ((a.N + COOP_WAVES_SEL - 1) / COOP_WAVES_SEL + 63) & ~int64_t(63);
+  const int64_t c_lo = int64_t(wave) * span, c_hi = min<int64_t>(a.N, c_lo + span);
+  auto unprotected = [&](int64_t c) { return c < c_hi && !(words[c >> 5] >> (c & 31) & 1u); };
+  int mine = 0;
+  for (int64_t c0 = c_lo; c0 < c_hi; c0 += 64) mine += __popcll(__ballot(unprotected(c0 + lane)));
+  int64_t j = wave_range_offset(mine, tmp);
+  for (int64_t c0 = c_lo; c0 < c_hi; c0 += 64) {
+    const int64_t c = c0 + lane;
+    const bool un = unprotected(c);
+    const uint64_t m = __ballot(un);
+    if (un) {
+      const int32_t sl = a.slots[c];
+      const int64_t r = j + __popcll(m & lanes_below());
+      if (r < width) {
+        a.targets[r] = sl;
+        trow[Q + r] = sl;
       } else {
-        a.leftover[j - width] = int64_t(sl[t]);
+        a.leftover[r - width] = int64_t(sl);
       }
-      ++j;
     }
-    carry += total;
+    j += __popcll(m);
   }
   for (int i = threadIdx.x; i < P; i += SEL_THREADS) trow[i < Q ? i : width + i] = a.slots[a.prot_cols[i]];
   if (threadIdx.x == 0) {
@@ -1654,13 +1665,23 @@ __global__ __launch_bounds__(SEL_THREADS) void repack_kernel(LiveBatch b) {
     else return bitmap_load(&a.bitmap[s >> 5]) >> (s & 31) & 1u;
   };
   const int32_t* trow = a.table + int64_t(a.row) * a.table_stride;
-  // In-order compaction: contiguous ranges per thread keep the table order.
-  const int64_t per = (cnt + SEL_THREADS - 1) / SEL_THREADS;
-  const int64_t lo = threadIdx.x * per, hi = min(cnt, lo + per);
-  int c = 0;
-  for (int64_t i = lo; i < hi; ++i) c += !is_real(trow[i]);
-  int packed;
-  int j = block_exclusive_scan<SEL_THREADS>(c, tmp, &packed);
+  // In-order compaction by waves: wave w packs the table entries of its contiguous range, 64 at a
+  // time with a ballot (one entry per lane: loads and stores contiguous), after the counts of the
+  // ranges before it.
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t span = ((cnt + COOP_WAVES_SEL - 1) / COOP_WAVES_SEL + 63) & ~int64_t(63);
+  const int64_t i_lo = int64_t(wave) * span, i_hi = min<int64_t>(cnt, i_lo + span);
+  int mine = 0;
+  for (int64_t i0 = i_lo; i0 < i_hi; i0 += 64) {
+    const int64_t i = i0 + lane;
+    mine += __popcll(__ballot(i < i_hi && !is_real(trow[i])));
+  }
+  int64_t j = wave_range_offset(mine, tmp);
+  int packed = 0;
+  if (wave == COOP_WAVES_SEL - 1) packed = int(j) + mine;  // the last wave's range ends the table
+  if (lane == 0 && wave == COOP_WAVES_SEL - 1) tmp[16] = packed;
+  __syncthreads();
+  packed = tmp[16];
   if (threadIdx.x == 0) a.status->packed = packed;
   if (packed > a.true_len) {
     if (threadIdx.x == 0) a.status->state = GSE_BOUNDARY_ERR_PACKED;
@@ -1668,9 +1689,13 @@ __global__ __launch_bounds__(SEL_THREADS) void repack_kernel(LiveBatch b) {
   }
   // Rows [packed, true_len) become holes; [0, packed) get the packed slots.
   for (int64_t i = packed + threadIdx.x; i < a.true_len; i += SEL_THREADS) rrow[i] = 0;
-  for (int64_t i = lo; i < hi; ++i) {
-    const int64_t s = trow[i];
-    if (!is_real(s)) rrow[j++] = int32_t(s);
+  for (int64_t i0 = i_lo; i0 < i_hi; i0 += 64) {
+    const int64_t i = i0 + lane;
+    const int32_t sl = i < i_hi ? trow[i] : 0;
+    const bool keep = i < i_hi && !is_real(sl);
+    const uint64_t m = __ballot(keep);
+    if (keep) rrow[j + __popcll(m & lanes_below())] = sl;
+    j += __popcll(m);
   }
 }
 
