@@ -1481,7 +1481,18 @@ __global__ void table_columns_kernel(BndBatch b) {
   float* out = reinterpret_cast<float*>(r.ws + L.col32);
   const int kv_heads = b.c.kv_heads;
   const float* row = b.c.scores + int64_t(l) * b.c.ssl + int64_t(slots[c]) * b.c.sss;
-  for (int g = 0; g < kv_heads; ++g) out[(int64_t(l) * kv_heads + g) * r.N + c] = row[int64_t(g) * b.c.ssg];
+  float* col = out + int64_t(l) * kv_heads * r.N + c;
+  if (kv_heads == 8 && b.c.ssg == 1 && b.c.sss == 8 && (reinterpret_cast<uintptr_t>(b.c.scores) & 15) == 0) {
+    // The runtime's layout: a slot's 8 head scores are one aligned 32-byte row, two 16-byte loads.
+    const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(row), hi = *reinterpret_cast<const f32x4_t*>(row + 4);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      col[int64_t(g) * r.N] = lo[g];
+      col[int64_t(g + 4) * r.N] = hi[g];
+    }
+    return;
+  }
+  for (int g = 0; g < kv_heads; ++g) col[int64_t(g) * r.N] = row[int64_t(g) * b.c.ssg];
 }
 
 // ------------------------------------------------------ block policy scores --
