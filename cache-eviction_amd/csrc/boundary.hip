@@ -607,6 +607,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(Src src) {
 // are >= 0x80000000). lo and the position are recomputed from global memory, and
 // only for columns still tied with the threshold after the hi digits.
 constexpr int SEL_LDS_KEYS = 34816;  // 34 columns per thread
+constexpr int SEL_FEW_EVICTED = 4;    // at most this many evictions: minimum rounds, no radix passes
 
 GSE_DEVICE uint32_t ordered_f32(float f) {
   const uint32_t u = __float_as_uint(f);
@@ -845,7 +846,67 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
   int fixed = 0;
   const bool take_all = (k == M);
   int krem = k;
-  if (k > 0 && !take_all) {
+  if (k > 0 && !take_all && table_scores && M - k <= SEL_FEW_EVICTED) {
+    // Few evictions (one per boundary when a row evicts at every step): the e = M - k smallest
+    // composites (hi, position) one at a time, each the smallest above the one before, by a
+    // workgroup minimum over the columns; the kept set is then every composite above the e-th,
+    // which is the threshold (hi, 0, position + 1) with every digit fixed. Positions are read only
+    // for columns whose hi key ties the comparison.
+    uint32_t ph = 0;
+    int32_t pp = -1;
+    for (int round = 0; round < M - k; ++round) {
+      uint32_t bh = 0xffffffffu;
+      int bc = -1;
+      int32_t bp = -1;  // position of bc, read when a tie needs it
+      for (int kk = 0; kk < KPT; ++kk) {
+        const int c = col(kk);
+        if (c >= N) break;
+        const uint32_t hi = keys[c];
+        if (hi == 0 || (round > 0 && hi < ph)) continue;  // protected, or at most the previous
+        int32_t p = -1;
+        if (round > 0 && hi == ph) {
+          p = col_pos(a, lg, c);
+          if (p <= pp) continue;
+        }
+        if (hi < bh) {
+          bh = hi;
+          bc = c;
+          bp = p;
+        } else if (hi == bh) {
+          if (bp < 0) bp = col_pos(a, lg, bc);
+          if (p < 0) p = col_pos(a, lg, c);
+          if (p < bp) {
+            bc = c;
+            bp = p;
+          }
+        }
+      }
+      if (bc >= 0 && bp < 0) bp = col_pos(a, lg, bc);
+      uint64_t best = bc >= 0 ? (uint64_t(bh) << 32) | uint32_t(bp) : ~0ull;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y = __shfl_xor(best, o, 64);
+        best = y < best ? y : best;
+      }
+      __syncthreads();  // the previous round's reads of the wave minima are done
+      if (lane == 0) {
+        redu[0][wave] = uint32_t(best >> 32);
+        redu[1][wave] = uint32_t(best);
+      }
+      __syncthreads();
+      best = ~0ull;
+      for (int w = 0; w < SEL_THREADS / 64; ++w) {
+        const uint64_t y = (uint64_t(redu[0][w]) << 32) | redu[1][w];
+        best = y < best ? y : best;
+      }
+      ph = uint32_t(best >> 32);
+      pp = int32_t(uint32_t(best));
+    }
+    th = ph;
+    tl = 0;
+    tp = uint32_t(pp) + 1;
+    fixed = 12;
+  } else if (k > 0 && !take_all) {
     const uint32_t diff = kand ^ kor;
     const int common = diff ? __clz(diff) / 8 : 4;  // leading hi bytes equal for all
     th = kand & (common >= 4 ? 0xffffffffu : ~(0xffffffffu >> (8 * common)));
