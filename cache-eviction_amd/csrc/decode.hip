@@ -604,11 +604,19 @@ __global__ void norm_from_lse_kernel(NormArgs a) {
   a.norm[int64_t(b) * a.q_heads + h] = m + logf(s);
 }
 
+// gse_decode_noalloc's partials and normalisers: one copy per GPU, held until the process ends.
+// In host code the name is a stand-in, not a device address: the library passes kernels the
+// address hipGetSymbolAddress gives for the current device (noalloc_scratch).
+static __device__ __align__(256) float scratch[GSE_DECODE_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
 }  // namespace gse
 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+#include <cstdio>
+#include <mutex>
+
 #include "host.hpp"
 
 using namespace gse;
@@ -652,21 +660,18 @@ extern "C" int64_t gse_decode_workspace_bytes(int bs, int q_heads, int head_dim)
   return parts * q_heads * (head_dim + 4) * int64_t(sizeof(float)) + int64_t(bs) * q_heads * 4;
 }
 
-extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                          const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
-                          const int32_t* kv_indptr, const void* kv_indices, int indices_dtype,
-                          const void* sinks, int sinks_dtype, const int32_t* mode_by_row, const void* rows,
-                          int rows_dtype, float* scores, int64_t scores_stride_g, int64_t scores_stride_s,
-                          void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
-                          void* queue_q, float* queue_norm, int32_t* queue_lim, int32_t* queue_count, int queue_cap,
-                          int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int max_len,
-                          int score_mode, float* logits, const int32_t* logit_index, int logit_rows, int logit_cap,
-                          void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
-  if (int rc = check_decode_shape(q_heads, kv_heads, head_dim)) return rc;
-  if (bs < 0) return gse_fail(GSE_EINVAL, "decode: bs < 0");
-  if (bs == 0) return GSE_OK;
-  if (workspace_bytes < gse_decode_workspace_bytes(bs, q_heads, head_dim))
-    return gse_fail(GSE_EWORKSPACE, "decode: workspace too small");
+namespace {
+
+// The decode launches over a workspace of at least gse_decode_workspace_bytes(bs, ...) bytes
+// (the caller's, or the library's scratch); shapes and bs > 0 are checked by the caller.
+int decode_run(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_pool, const void* v_pool,
+               int64_t kv_stride_s, int64_t kv_stride_h, const int32_t* kv_indptr, const void* kv_indices,
+               int indices_dtype, const void* sinks, int sinks_dtype, const int32_t* mode_by_row, const void* rows,
+               int rows_dtype, float* scores, int64_t scores_stride_g, int64_t scores_stride_s, void* o,
+               int64_t o_stride_b, int64_t o_stride_h, float* norm_out, void* queue_q, float* queue_norm,
+               int32_t* queue_lim, int32_t* queue_count, int queue_cap, int bs, int q_heads, int kv_heads,
+               float sm_scale, int max_len, int score_mode, float* logits, const int32_t* logit_index,
+               int logit_rows, int logit_cap, void* workspace, gse_stream_t stream) {
   if (!q || !k_pool || !v_pool || !kv_indptr || !kv_indices || !sinks || !o)
     return gse_fail(GSE_EINVAL, "decode: null pointer");
   if (score_mode < GSE_SCORE_NONE || score_mode > GSE_SCORE_QUEUE) return gse_fail(GSE_EINVAL, "decode: bad score_mode");
@@ -765,6 +770,84 @@ extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
     if ((rc = score_pass(sa, indices_dtype, bs, max_len, s))) return rc;
   }
   return GSE_OK;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device with it current.
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return gse_fail(GSE_ELAUNCH, "decode_noalloc: no current HIP device (or a device id >= 64)");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return gse_fail(GSE_ELAUNCH, "decode_noalloc: hipGetSymbolAddress of the scratch array failed");
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GSE_OK;
+}
+
+}  // namespace
+
+extern "C" int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                          const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
+                          const int32_t* kv_indptr, const void* kv_indices, int indices_dtype,
+                          const void* sinks, int sinks_dtype, const int32_t* mode_by_row, const void* rows,
+                          int rows_dtype, float* scores, int64_t scores_stride_g, int64_t scores_stride_s,
+                          void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
+                          void* queue_q, float* queue_norm, int32_t* queue_lim, int32_t* queue_count, int queue_cap,
+                          int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int max_len,
+                          int score_mode, float* logits, const int32_t* logit_index, int logit_rows, int logit_cap,
+                          void* workspace, int64_t workspace_bytes, gse_stream_t stream) {
+  if (int rc = check_decode_shape(q_heads, kv_heads, head_dim)) return rc;
+  if (bs < 0) return gse_fail(GSE_EINVAL, "decode: bs < 0");
+  if (bs == 0) return GSE_OK;
+  if (workspace_bytes < gse_decode_workspace_bytes(bs, q_heads, head_dim))
+    return gse_fail(GSE_EWORKSPACE, "decode: workspace too small");
+  if (!workspace) return gse_fail(GSE_EINVAL, "decode: null workspace");
+  return decode_run(q, q_stride_b, q_stride_h, k_pool, v_pool, kv_stride_s, kv_stride_h, kv_indptr, kv_indices,
+                    indices_dtype, sinks, sinks_dtype, mode_by_row, rows, rows_dtype, scores, scores_stride_g,
+                    scores_stride_s, o, o_stride_b, o_stride_h, norm_out, queue_q, queue_norm, queue_lim, queue_count,
+                    queue_cap, bs, q_heads, kv_heads, sm_scale, max_len, score_mode, logits, logit_index, logit_rows,
+                    logit_cap, workspace, stream);
+}
+
+extern "C" int gse_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                  const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
+                                  const int32_t* kv_indptr, const void* kv_indices, int indices_dtype,
+                                  const void* sinks, int sinks_dtype, const int32_t* mode_by_row, const void* rows,
+                                  int rows_dtype, float* scores, int64_t scores_stride_g, int64_t scores_stride_s,
+                                  void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
+                                  void* queue_q, float* queue_norm, int32_t* queue_lim, int32_t* queue_count,
+                                  int queue_cap, int bs, int q_heads, int kv_heads, int head_dim, float sm_scale,
+                                  int max_len, int score_mode, float* logits, const int32_t* logit_index,
+                                  int logit_rows, int logit_cap, gse_stream_t stream) {
+  if (int rc = check_decode_shape(q_heads, kv_heads, head_dim)) return rc;
+  if (bs < 0) return gse_fail(GSE_EINVAL, "decode_noalloc: bs < 0");
+  if (bs == 0) return GSE_OK;
+  const int64_t need = gse_decode_workspace_bytes(bs, q_heads, head_dim);
+  if (need > int64_t(GSE_DECODE_NOALLOC_SCRATCH_BYTES)) {
+    char msg[256];
+    snprintf(msg, sizeof(msg),
+             "decode_noalloc: bs=%d with %d query heads needs %lld bytes of scratch, more than the library's %lld "
+             "(GSE_DECODE_NOALLOC_SCRATCH_BYTES); use gse_decode with a workspace",
+             bs, q_heads, static_cast<long long>(need), static_cast<long long>(GSE_DECODE_NOALLOC_SCRATCH_BYTES));
+    return gse_fail(GSE_EWORKSPACE, msg);
+  }
+  void* ws = nullptr;
+  if (int rc = noalloc_scratch(&ws)) return rc;
+  return decode_run(q, q_stride_b, q_stride_h, k_pool, v_pool, kv_stride_s, kv_stride_h, kv_indptr, kv_indices,
+                    indices_dtype, sinks, sinks_dtype, mode_by_row, rows, rows_dtype, scores, scores_stride_g,
+                    scores_stride_s, o, o_stride_b, o_stride_h, norm_out, queue_q, queue_norm, queue_lim, queue_count,
+                    queue_cap, bs, q_heads, kv_heads, sm_scale, max_len, score_mode, logits, logit_index, logit_rows,
+                    logit_cap, ws, stream);
 }
 
 extern "C" int gse_decode_scores_from_lse(const void* q, int64_t q_stride_b, int64_t q_stride_h,

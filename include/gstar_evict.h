@@ -188,6 +188,32 @@ int gse_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                int score_mode, float* logits, const int32_t* logit_index, int logit_rows, int logit_cap,
                void* workspace, int64_t workspace_bytes, gse_stream_t stream);
 
+/* Bytes of the library's own scratch for gse_decode_noalloc on each GPU (9 MiB: bs <= 256 at
+ * 64 query heads on 256 CUs). */
+#define GSE_DECODE_NOALLOC_SCRATCH_BYTES (9 * 1024 * 1024)
+
+/*
+ * decode_noalloc — gse_decode without a workspace argument, allocating nothing: no counterpart
+ * in the reference. For callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation). Same arguments (less the workspace), result
+ * and kernels as gse_decode; the partials live in a static device array of
+ * GSE_DECODE_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, whose address is looked
+ * up once per device on its first call there. Returns GSE_EWORKSPACE (no launch) when
+ * gse_decode_workspace_bytes(bs, q_heads, head_dim) exceeds that size. Every call on one GPU
+ * shares its array: calls that overlap on one GPU (other streams, other threads) race, so
+ * order them on one stream.
+ */
+int gse_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                       const void* k_pool, const void* v_pool, int64_t kv_stride_s, int64_t kv_stride_h,
+                       const int32_t* kv_indptr, const void* kv_indices, int indices_dtype,
+                       const void* sinks, int sinks_dtype, const int32_t* mode_by_row, const void* rows,
+                       int rows_dtype, float* scores, int64_t scores_stride_g, int64_t scores_stride_s,
+                       void* o, int64_t o_stride_b, int64_t o_stride_h, float* norm_out,
+                       void* queue_q, float* queue_norm, int32_t* queue_lim, int32_t* queue_count, int queue_cap,
+                       int bs, int q_heads, int kv_heads, int head_dim, float sm_scale, int max_len,
+                       int score_mode, float* logits, const int32_t* logit_index, int logit_rows, int logit_cap,
+                       gse_stream_t stream);
+
 /*
  * score_flush — add the queued decode scores of the listed rows, for every full
  * layer, and empty their queues. No reference counterpart as an entry point: the

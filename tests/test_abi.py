@@ -124,6 +124,22 @@ def test_logit_flush_rejects_bad_arguments_without_a_gpu():
     assert rc != 0 and b"kept logits" in lib.gse_last_error()
 
 
+def test_noalloc_decode_refuses_a_batch_beyond_its_scratch_without_a_gpu():
+    """bs = 1024 at 64 query heads needs more partials than the static scratch holds: refused
+    before any device call."""
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    lib = _native.lib()
+    assert lib.gse_decode_workspace_bytes(1024, 64, 64) > (9 << 20)
+    buf = ctypes.create_string_buffer(256)
+    p = ctypes.addressof(buf)
+    rc = lib.gse_decode_noalloc(p, 0, 0, p, p, 0, 0, p, p, 0, p, 0, p, p, 0, None, 0, 1, p, 0, 0, None, p, p, p, p,
+                                4, 1024, 64, 8, 64, 0.125, 512, 2, None, None, 0, 0, None)
+    assert rc != 0
+    msg = lib.gse_last_error()
+    assert b"GSE_DECODE_NOALLOC_SCRATCH_BYTES" in msg and b"bs=1024" in msg
+
+
 def test_row_descriptors_match_the_header_layout(tmp_path):
     """The ctypes mirrors of gse_boundary_row and gse_live_row have the C structs' size and
     field offsets (a C program built against the header reports them)."""

@@ -1,0 +1,104 @@
+"""gse_decode_noalloc (the decode entry point that allocates nothing: its partials live in the
+library's static scratch array) against gse_decode with a caller workspace, through the C ABI.
+
+Both run the same kernels over the same inputs, so every output matches bit for bit: attention
+output, normalisers, queued steps, kept products and eager scores (each slot of these lists is
+distinct, so an eager score is one addition to zero). Two calls in a row, the second with a
+smaller batch, show that nothing depends on what the scratch held before."""
+import numpy as np
+import pytest
+import torch
+
+from gstar_evict import _native as N
+
+pytestmark = pytest.mark.gpu
+
+HEADS, KV_HEADS, DIM, ROWS, CAP = 64, 8, 64, 10, 4
+# (lengths, rows): a ragged batch of 8 with a length-1 list, then a smaller one of 3.
+CASES = [([9000, 300, 15000, 4096, 1, 7777, 12000, 2500], [1, 2, 3, 4, 5, 6, 7, 8]),
+         ([640, 2049, 33], [3, 9, 1])]
+SLOTS = 60000
+
+
+@pytest.fixture(scope="module")
+def pools():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    g = torch.Generator().manual_seed(7)
+    k = torch.randn((SLOTS, KV_HEADS, DIM), generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn((SLOTS, KV_HEADS, DIM), generator=g).to(torch.bfloat16).cuda()
+    sinks = torch.randn(HEADS, generator=g).to(torch.bfloat16).cuda()
+    mode = torch.ones(ROWS, dtype=torch.int32)
+    mode[3] = 2  # row 3 takes the max over its heads
+    return g, k, v, sinks, mode.cuda()
+
+
+def _inputs(g, lengths, rows):
+    total = sum(lengths)
+    assert total <= SLOTS - 1, "every list entry needs its own slot"
+    indices = (torch.randperm(SLOTS - 1, generator=g)[:total] + 1).int()
+    assert indices.numel() == total
+    indptr = torch.tensor(np.concatenate(([0], np.cumsum(lengths))), dtype=torch.int32)
+    q = torch.randn((len(rows), HEADS, DIM), generator=g).to(torch.bfloat16)
+    return q.cuda(), indptr.cuda(), indices.cuda(), torch.tensor(rows, dtype=torch.int64).cuda()
+
+
+def _outputs(bs, lcap):
+    return dict(o=torch.full((bs, HEADS, DIM), 7.0, dtype=torch.bfloat16, device="cuda"),
+                norm=torch.full((bs, HEADS), 7.0, device="cuda"),
+                scores=torch.zeros((KV_HEADS, SLOTS), device="cuda"),
+                qq=torch.zeros((ROWS, CAP, HEADS, DIM), dtype=torch.bfloat16, device="cuda"),
+                qnorm=torch.zeros((ROWS, CAP, HEADS), device="cuda"),
+                qlim=torch.zeros((ROWS, CAP), dtype=torch.int32, device="cuda"),
+                qcount=torch.zeros(ROWS, dtype=torch.int32, device="cuda"),
+                logits=torch.full((2, KV_HEADS, lcap, 8), 7.0, device="cuda"))
+
+
+def _call(name, pools, inputs, out, score_mode, max_len, lidx, lcap):
+    _, k, v, sinks, mode = pools
+    q, indptr, indices, rows = inputs
+    bs = q.shape[0]
+    # The lists must fit the pools and the index array before any launch.
+    assert int(indptr[-1]) == indices.numel() and int(indices.max()) < SLOTS and int(rows.max()) < ROWS
+    head = (N.ptr(q), q.stride(0), q.stride(1), N.ptr(k), N.ptr(v), k.stride(0), k.stride(1), N.ptr(indptr),
+            N.ptr(indices), N.idx_code(indices), N.ptr(sinks), N.float_code(sinks), N.ptr(mode), N.ptr(rows),
+            N.idx_code(rows), N.ptr(out["scores"]), out["scores"].stride(0), out["scores"].stride(1),
+            N.ptr(out["o"]), out["o"].stride(0), out["o"].stride(1), N.ptr(out["norm"]), N.ptr(out["qq"]),
+            N.ptr(out["qnorm"]), N.ptr(out["qlim"]), N.ptr(out["qcount"]), CAP, bs, HEADS, KV_HEADS, DIM, 0.125,
+            max_len, score_mode, N.ptr(out["logits"]), N.ptr(lidx), 2, lcap)
+    if name == "gse_decode":
+        nbytes = N.lib().gse_decode_workspace_bytes(bs, HEADS, DIM)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        N.call(name, *head, N.ptr(ws), nbytes, N.stream())
+    else:
+        N.call(name, *head, N.stream())
+
+
+@pytest.mark.parametrize("score_mode", [2, 1])  # queued steps, then eager scores
+def test_noalloc_decode_equals_decode_on_two_calls_in_a_row(pools, score_mode):
+    g = pools[0]
+    for lengths, rows in CASES:
+        print(f"noalloc decode: score_mode={score_mode} bs={len(lengths)} lengths={lengths}", flush=True)
+        inputs = _inputs(g, lengths, rows)
+        max_len = max(lengths)
+        lcap = 4096  # products of the first 4096 entries of the kept rows
+        lidx = torch.full((ROWS,), -1, dtype=torch.int32, device="cuda")
+        lidx[rows[0]], lidx[rows[-1]] = 0, 1
+        got = {}
+        for name in ("gse_decode", "gse_decode_noalloc"):
+            out = _outputs(len(lengths), lcap)
+            _call(name, pools, inputs, out, score_mode, max_len, lidx, lcap)
+            torch.cuda.synchronize()
+            got[name] = out
+        a, b = got["gse_decode"], got["gse_decode_noalloc"]
+        assert bool((a["o"] != 7).all()) and bool((a["norm"] != 7).all())  # every output written
+        for k, n in ((0, lengths[0]), (1, lengths[-1])):  # kept products of the first and last sequence
+            n = min(n, lcap)
+            assert bool((a["logits"][k, :, :n] != 7).all()) and bool((a["logits"][k, :, n:] == 7).all())
+        if score_mode == 2:
+            assert a["qcount"][rows].tolist() == [1] * len(rows)
+        else:
+            assert float(a["scores"].abs().sum()) > 0
+        for key in a:
+            assert torch.equal(a[key], b[key]), key
+
