@@ -1434,7 +1434,6 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
   // Entries, and so their targets, are the same for the whole wave (scalar registers).
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t j0 = (int64_t(blockIdx.x) * COOP_WAVES + wave) * per;
-  const int64_t off = int64_t(g) * a.kv_sh + 8 * piece;
   // Entry r of the wave is j0 + r up to its last one, min(j0 + per, width) - 1; the spare
   // registers repeat that last entry (a wave with none repeats entries spread over the width),
   // and a repeat moves the same bytes to the same target in the same phase as the entry's own
@@ -1445,34 +1444,77 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
 #pragma unroll
   for (int r = 0; r < PER; ++r) {
     jc[r] = int32_t(j0 + r <= last ? j0 + r : (j0 < width ? last : (j0 + r) % width));
-    dst[r] = a.targets[jc[r]];
+    dst[r] = __builtin_amdgcn_readfirstlane(a.targets[jc[r]]);  // one target per entry
   }
+  // A head's entry whose source is its target (every kept entry before the head's first evicted
+  // column) moves nothing: its lanes neither load nor store. K and V go through buffer
+  // instructions indexed by slot (stride = the slot row, so any int32 slot is addressable) and
+  // the scores through byte offsets within the layer; a lane that does not move gives an index
+  // and offset past every bound, and the hardware's range check drops its access (a load returns
+  // 0). Every instruction stays unconditional, so the waits stay exact. A move map holds bit r
+  // for entry r of the lane's head: `cur` for the layer being stored, `next` for the one being
+  // loaded.
   int32_t src[PER];
+  uint32_t cur = 0, next = 0;
   uint4 kd[PER], vd[PER];
   float sc[PER];
+  const int32_t lane_bytes = int32_t(g) * int32_t(a.kv_sh) * 2 + 16 * piece;  // within a slot row
+  const uint32_t score_lane = uint32_t(g) * uint32_t(a.ssg) * 4u, score_slot = uint32_t(a.sss) * 4u;
+  auto kv_rsrc = [&](const uint16_t* pool) {
+    const uint64_t p = reinterpret_cast<uint64_t>(pool);
+    // readfirstlane returns int: each half goes through uint32_t, or the low half's sign would
+    // fill the high word.
+    const uint64_t u = uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(p >> 32)))) << 32 |
+                       uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(p))));
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), int16_t(a.kv_ss * 2), INT32_MAX,
+                                             BUFFER_RSRC_FLAGS);
+  };
+  auto score_rsrc = [&](int l) {
+    return __builtin_amdgcn_make_buffer_rsrc(a.scores + int64_t(l) * a.ssl, 0, INT32_MAX, BUFFER_RSRC_FLAGS);
+  };
+  auto moves = [](uint32_t map, int r) { return ((map >> r) & 1u) != 0; };
+  const uint32_t mrow = uint32_t(g) * uint32_t(a.budget) * 4u;
+  auto at = [](const int32_t* p, uint32_t bytes) { return reinterpret_cast<const int32_t*>(reinterpret_cast<const char*>(p) + bytes); };
   auto sources = [&](int l) {
-    const int32_t* m = a.middle + int64_t(l * a.kv_heads + g) * a.budget;
+    const int32_t* m = a.middle + int64_t(l * a.kv_heads) * a.budget;
+    int32_t col[PER];
 #pragma unroll
-    for (int r = 0; r < PER; ++r) src[r] = a.slots[m[jc[r]]];
+    for (int r = 0; r < PER; ++r) col[r] = *at(m + jc[r], mrow);
+    __builtin_amdgcn_sched_barrier(0);  // all column loads before their first use
+#pragma unroll
+    for (int r = 0; r < PER; ++r) src[r] = *at(a.slots, uint32_t(col[r]) * 4u);
+  };
+  // After sources(), once its loads have landed (just before the K loads that use them).
+  auto mark = [&]() {
+    next = 0;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) next |= uint32_t(src[r] != dst[r]) << r;
   };
   auto load_k = [&](int l) {
-    auto K = as_global(static_cast<const uint16_t*>(pools[0][l]));
-    const float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
+    const auto K = kv_rsrc(pools[0][l]);
+    const auto S = score_rsrc(l);
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
-      kd[r] = gload16_nt(K + int64_t(src[r]) * a.kv_ss + off);
-      sc[r] = srow[int64_t(src[r]) * a.sss];
+      const bool mv = moves(next, r);
+      kd[r] = buffer_load16_nt(K, mv ? src[r] : BUFFER_NO_INDEX, mv ? lane_bytes : BUFFER_OUT_OF_RANGE);
+      uint32_t so = opaque(uint32_t(src[r]) * score_slot) + score_lane;
+      sc[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(S, mv ? int(so) : BUFFER_OUT_OF_RANGE, 0, 0));
     }
   };
   auto load_v = [&](int l) {
-    auto V = as_global(static_cast<const uint16_t*>(pools[1][l]));
+    const auto V = kv_rsrc(pools[1][l]);
 #pragma unroll
-    for (int r = 0; r < PER; ++r) vd[r] = gload16_nt(V + int64_t(src[r]) * a.kv_ss + off);
+    for (int r = 0; r < PER; ++r) {
+      const bool mv = moves(cur, r);
+      vd[r] = buffer_load16_nt(V, mv ? src[r] : BUFFER_NO_INDEX, mv ? lane_bytes : BUFFER_OUT_OF_RANGE);
+    }
   };
   bool gave_up = false;
   sources(0);
+  mark();
   load_k(0);
   for (int l = 0; l < a.layers; ++l) {
+    cur = next;
     // Phase 2l: layer l's K rows and scores.
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
@@ -1487,24 +1529,32 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
       return;
     }
     {
-      auto K = as_global(pools[0][l]);
-      float* srow = a.scores + int64_t(l) * a.ssl + int64_t(g) * a.ssg;
+      const auto K = kv_rsrc(pools[0][l]);
+      const auto S = score_rsrc(l);
 #pragma unroll
       for (int r = 0; r < PER; ++r) {
-        gstore16_nt(K + int64_t(dst[r]) * a.kv_ss + off, kd[r]);
-        srow[int64_t(dst[r]) * a.sss] = sc[r];
+        const bool mv = moves(cur, r);
+        buffer_store16_nt(kd[r], K, mv ? dst[r] : BUFFER_NO_INDEX, mv ? lane_bytes : BUFFER_OUT_OF_RANGE);
+        const uint32_t so = uint32_t(dst[r]) * score_slot + score_lane;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sc[r]), S, mv ? int(so) : BUFFER_OUT_OF_RANGE, 0, 0);
       }
     }
     // Phase 2l + 1: layer l's V rows.
 #pragma unroll
     for (int r = 0; r < PER; ++r) landed(vd[r]);
     grid_arrive(a, uint32_t(2 * l + 1));
-    if (l + 1 < a.layers) load_k(l + 1);
+    if (l + 1 < a.layers) {
+      mark();
+      load_k(l + 1);
+    }
     grid_wait(a, uint32_t(2 * l + 1), gave_up, &go);
     {
-      auto V = as_global(pools[1][l]);
+      const auto V = kv_rsrc(pools[1][l]);
 #pragma unroll
-      for (int r = 0; r < PER; ++r) gstore16_nt(V + int64_t(dst[r]) * a.kv_ss + off, vd[r]);
+      for (int r = 0; r < PER; ++r) {
+        const bool mv = moves(cur, r);
+        buffer_store16_nt(vd[r], V, mv ? dst[r] : BUFFER_NO_INDEX, mv ? lane_bytes : BUFFER_OUT_OF_RANGE);
+      }
     }
   }
 }
@@ -2034,7 +2084,13 @@ int boundary_impl(void* const* k_pools, void* const* v_pools, int layers, int64_
   c.scratch_kv = reinterpret_cast<uint16_t*>(ws);
   c.scratch_sc = reinterpret_cast<float*>(ws + align256(LG * budget * 2 * head_dim * 2));
   int coop_blocks = 0, coop_per = 0;
-  if (kv_heads == 8 && head_dim == 64 && layers <= COOP_MAX_LAYERS) coop_plan(budget, &coop_blocks, &coop_per);
+  // The single pass addresses K and V rows as records of a structured buffer (the slot stride in
+  // bytes must fit the descriptor's 14-bit stride field) and scores by byte offsets within one
+  // layer (below 2 GiB).
+  const bool coop_offsets = c.kv_ss > 0 && c.kv_ss * 2 < (1 << 14) && c.kv_sh >= 0 && c.ssl > 0 &&
+                            c.ssl < (int64_t(1) << 29) && c.ssg >= 0 && c.sss >= 0;
+  if (kv_heads == 8 && head_dim == 64 && layers <= COOP_MAX_LAYERS && coop_offsets)
+    coop_plan(budget, &coop_blocks, &coop_per);
   c.relocation = coop_blocks > 0 ? GSE_RELOCATION_SINGLE_PASS : GSE_RELOCATION_SCRATCH;
   c.coop_spin_limit = COOP_SPIN_LIMIT;
   c.coop_extra_target = 0;

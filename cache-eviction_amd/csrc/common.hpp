@@ -111,6 +111,37 @@ GSE_DEVICE void gstore16_nt(__attribute__((address_space(1))) void* p, uint4 v) 
   __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), (__attribute__((address_space(1))) u32x4_t*)p);
 }
 
+// Buffer resources (word 3 of the descriptor as gfx9-family parts take it). The hardware's range
+// check drops an access that is out of range (a load returns 0, a store writes nothing): with
+// stride 0 (raw) an offset at or past num_records, with a stride (structured) an index at or past
+// num_records. Code that must not touch memory for some lanes gives those lanes
+// BUFFER_NO_INDEX and BUFFER_OUT_OF_RANGE, past both bounds.
+constexpr int BUFFER_RSRC_FLAGS = 0x00020000;
+constexpr int BUFFER_OUT_OF_RANGE = int(0x80000000u);
+constexpr int BUFFER_NO_INDEX = int(0xFFFFFFFFu);
+constexpr int BUFFER_NT = 2;  // cache policy: nontemporal
+
+// 16 bytes at record `index`, byte `offset` of a structured buffer (the LLVM intrinsic; clang has
+// builtins for the raw forms only).
+GSE_DEVICE u32x4_t struct_buffer_load_b128(__amdgpu_buffer_rsrc_t rsrc, int index, int offset, int soffset,
+                                           int aux) __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
+GSE_DEVICE void struct_buffer_store_b128(u32x4_t v, __amdgpu_buffer_rsrc_t rsrc, int index, int offset,
+                                         int soffset, int aux) __asm("llvm.amdgcn.struct.ptr.buffer.store.v4i32");
+GSE_DEVICE uint4 buffer_load16_nt(__amdgpu_buffer_rsrc_t rsrc, int index, int offset) {
+  return __builtin_bit_cast(uint4, struct_buffer_load_b128(rsrc, index, offset, 0, BUFFER_NT));
+}
+GSE_DEVICE void buffer_store16_nt(uint4 v, __amdgpu_buffer_rsrc_t rsrc, int index, int offset) {
+  struct_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rsrc, index, offset, 0, BUFFER_NT);
+}
+
+// A value the compiler cannot see through: keeps a 32-bit product from being fused with a later
+// add into a 64-bit multiply-add, whose unused high addend register the wait counting treats as
+// read (it then waits for whatever load last wrote that register).
+GSE_DEVICE uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 template <typename T>
 GSE_DEVICE int64_t load_index(const void* p, int64_t i) {
   return int64_t(static_cast<const T*>(p)[i]);

@@ -29,11 +29,6 @@ constexpr int FUSED_THREADS = 64 * MAX_KVH;
 
 GSE_DEVICE uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
-// Raw buffer resources (stride 0, word 3 of the descriptor as gfx9-family parts take it): an
-// access whose offset is at or past num_records is dropped by the hardware's range check.
-constexpr int BUFFER_RSRC_FLAGS = 0x00020000;
-constexpr int BUFFER_OUT_OF_RANGE = int(0x80000000u);
-
 
 // Keys per workgroup for P workgroups over T keys (0 when T == 0).
 GSE_DEVICE int fused_chunk(int T, int P) { return (T + P - 1) / P; }
