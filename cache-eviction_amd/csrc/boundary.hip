@@ -1049,6 +1049,10 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
 // 1.3 TB/s). Polls sleep 20 x 64 cycles between reads.
 constexpr int COOP_THREADS = 1024;
 constexpr int COOP_WAVES_SEL = SEL_THREADS / 64;  // waves of a SEL_THREADS workgroup
+// Chunks of 64 entries whose loads a wave issues together before using them, in the per-row
+// compaction loops (one round trip per batch instead of one per chunk: the stores between chunks
+// could alias the next chunk's loads, so the compiler keeps them in program order).
+constexpr int LOAD_BATCH = 16;
 constexpr int COOP_WAVES = COOP_THREADS / 64;
 constexpr int COOP_SLEEP = 20;
 constexpr int COOP_SPIN_LIMIT = 1 << 18;
@@ -1135,9 +1139,16 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndBatch b) {
   const int Q = a.prot_low[0];
   for (int i = threadIdx.x; i < a.nwords_cols; i += SEL_THREADS) words[i] = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < P; i += SEL_THREADS) {
-    const int c = a.prot_cols[i];
-    atomicOr(&words[c >> 5], 1u << (c & 31));
+  for (int i0 = 0; i0 < P; i0 += SEL_THREADS * LOAD_BATCH) {
+    int c[LOAD_BATCH];
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) {
+      const int i = i0 + k * SEL_THREADS + threadIdx.x;
+      c[k] = i < P ? a.prot_cols[i] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k)
+      if (c[k] >= 0) atomicOr(&words[c[k] >> 5], 1u << (c[k] & 31));
   }
   __syncthreads();
   int32_t* trow = a.table + int64_t(a.row) * a.table_stride;
@@ -1152,23 +1163,45 @@ __global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndBatch b) {
   int mine = 0;
   for (int64_t c0 = c_lo; c0 < c_hi; c0 += 64) mine += __popcll(__ballot(unprotected(c0 + lane)));
   int64_t j = wave_range_offset(mine, tmp);
-  for (int64_t c0 = c_lo; c0 < c_hi; c0 += 64) {
-    const int64_t c = c0 + lane;
-    const bool un = unprotected(c);
-    const uint64_t m = __ballot(un);
-    if (un) {
-      const int32_t sl = a.slots[c];
-      const int64_t r = j + __popcll(m & lanes_below());
-      if (r < width) {
-        a.targets[r] = sl;
-        trow[Q + r] = sl;
-      } else {
-        a.leftover[r - width] = int64_t(sl);
-      }
+  for (int64_t b0 = c_lo; b0 < c_hi; b0 += 64 * LOAD_BATCH) {
+    int32_t sl[LOAD_BATCH];
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) {
+      const int64_t c = b0 + 64 * k + lane;
+      sl[k] = c < c_hi ? a.slots[c] : 0;
     }
-    j += __popcll(m);
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) {
+      const int64_t c = b0 + 64 * k + lane;
+      const bool un = unprotected(c);
+      const uint64_t m = __ballot(un);
+      if (un) {
+        const int64_t r = j + __popcll(m & lanes_below());
+        if (r < width) {
+          a.targets[r] = sl[k];
+          trow[Q + r] = sl[k];
+        } else {
+          a.leftover[r - width] = int64_t(sl[k]);
+        }
+      }
+      j += __popcll(m);
+    }
   }
-  for (int i = threadIdx.x; i < P; i += SEL_THREADS) trow[i < Q ? i : width + i] = a.slots[a.prot_cols[i]];
+  for (int i0 = 0; i0 < P; i0 += SEL_THREADS * LOAD_BATCH) {
+    int c[LOAD_BATCH], sv[LOAD_BATCH];
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) {
+      const int i = i0 + k * SEL_THREADS + threadIdx.x;
+      c[k] = i < P ? a.prot_cols[i] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) sv[k] = a.slots[c[k]];
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) {
+      const int i = i0 + k * SEL_THREADS + threadIdx.x;
+      if (i < P) trow[i < Q ? i : width + i] = sv[k];
+    }
+  }
   if (threadIdx.x == 0) {
     a.count[a.row] = int32_t(P + width);
     a.frontier[a.row] = int32_t(a.n);
@@ -1568,10 +1601,25 @@ __global__ __launch_bounds__(256) void protected_pos_kernel(BndBatch b) {
   if (st.state != GSE_BOUNDARY_EVICTED) return;
   const int lg = blockIdx.x;
   const int Q = a.prot_low[0];
-  for (int i = threadIdx.x; i < st.protected_count; i += blockDim.x) {
-    const int64_t c = a.prot_cols[i];
-    const int64_t p = c < a.row_count ? int64_t(a.pos_old[int64_t(lg) * a.pstride + c]) : a.row_frontier + c - a.row_count;
-    a.pos_new[int64_t(lg) * a.budget + (i < Q ? i : st.width + i)] = int32_t(p);
+  constexpr int B = 8;  // protected columns per thread whose loads issue together
+  const int P = st.protected_count;
+  for (int i0 = 0; i0 < P; i0 += 256 * B) {
+    int64_t c[B];
+    int32_t old[B];
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+      const int i = i0 + k * 256 + int(threadIdx.x);
+      c[k] = i < P ? a.prot_cols[i] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < B; ++k) old[k] = c[k] < a.row_count ? a.pos_old[int64_t(lg) * a.pstride + c[k]] : 0;
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+      const int i = i0 + k * 256 + int(threadIdx.x);
+      if (i >= P) continue;
+      const int64_t p = c[k] < a.row_count ? int64_t(old[k]) : a.row_frontier + c[k] - a.row_count;
+      a.pos_new[int64_t(lg) * a.budget + (i < Q ? i : st.width + i)] = int32_t(p);
+    }
   }
 }
 
@@ -1794,9 +1842,15 @@ __global__ __launch_bounds__(SEL_THREADS) void repack_kernel(LiveBatch b) {
   const int64_t span = ((cnt + COOP_WAVES_SEL - 1) / COOP_WAVES_SEL + 63) & ~int64_t(63);
   const int64_t i_lo = int64_t(wave) * span, i_hi = min<int64_t>(cnt, i_lo + span);
   int mine = 0;
-  for (int64_t i0 = i_lo; i0 < i_hi; i0 += 64) {
-    const int64_t i = i0 + lane;
-    mine += __popcll(__ballot(i < i_hi && !is_real(trow[i])));
+  for (int64_t b0 = i_lo; b0 < i_hi; b0 += 64 * LOAD_BATCH) {
+    int32_t sl[LOAD_BATCH];
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) {
+      const int64_t i = b0 + 64 * k + lane;
+      sl[k] = i < i_hi ? trow[i] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) mine += __popcll(__ballot(b0 + 64 * k + lane < i_hi && !is_real(sl[k])));
   }
   int64_t j = wave_range_offset(mine, tmp);
   int packed = 0;
@@ -1811,13 +1865,20 @@ __global__ __launch_bounds__(SEL_THREADS) void repack_kernel(LiveBatch b) {
   }
   // Rows [packed, true_len) become holes; [0, packed) get the packed slots.
   for (int64_t i = packed + threadIdx.x; i < a.true_len; i += SEL_THREADS) rrow[i] = 0;
-  for (int64_t i0 = i_lo; i0 < i_hi; i0 += 64) {
-    const int64_t i = i0 + lane;
-    const int32_t sl = i < i_hi ? trow[i] : 0;
-    const bool keep = i < i_hi && !is_real(sl);
-    const uint64_t m = __ballot(keep);
-    if (keep) rrow[j + __popcll(m & lanes_below())] = sl;
-    j += __popcll(m);
+  for (int64_t b0 = i_lo; b0 < i_hi; b0 += 64 * LOAD_BATCH) {
+    int32_t sl[LOAD_BATCH];
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) {
+      const int64_t i = b0 + 64 * k + lane;
+      sl[k] = i < i_hi ? trow[i] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < LOAD_BATCH; ++k) {
+      const bool keep = b0 + 64 * k + lane < i_hi && !is_real(sl[k]);
+      const uint64_t m = __ballot(keep);
+      if (keep) rrow[j + __popcll(m & lanes_below())] = sl[k];
+      j += __popcll(m);
+    }
   }
 }
 
