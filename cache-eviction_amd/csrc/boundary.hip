@@ -780,16 +780,13 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
   };
 
   // Phase 1: hi keys, protection counts, common high bits of the unprotected keys. Also, for a
-  // boundary that evicts few columns: each thread's SEL_FEW_EVICTED smallest composites (hi,
-  // position) among its unprotected columns, ascending, with their columns, and the unprotected
-  // flag of every column in kbits (the kept flags once the evicted ones are cleared).
+  // boundary that evicts few columns: the thread's smallest composite (hi, position) among its
+  // unprotected columns and its column index, and the unprotected flag of every column in kbits
+  // (the kept flags once the evicted ones are cleared).
   int nprot = 0, nlow = 0;
   uint32_t kand = 0xffffffffu, kor = 0u;
-  static_assert(SEL_FEW_EVICTED == 4 && KPT < 256, "four candidate column indices, a byte each");
-  uint64_t fk[SEL_FEW_EVICTED];
-  uint32_t fc = 0;  // byte i: the column index kk (column col(kk)) of candidate i
-#pragma unroll
-  for (int i = 0; i < SEL_FEW_EVICTED; ++i) fk[i] = ~0ull;
+  uint64_t fmin = ~0ull;
+  int fkk = 0;
   for (int k0 = 0; k0 < KPT; k0 += BATCH) {
     int32_t pb[BATCH];
     load_pos(k0, pb);
@@ -816,20 +813,8 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
           kor |= hi;
           unprot = true;
           const uint64_t key = (uint64_t(hi) << 32) | uint32_t(pb[u]);
-          if (key < fk[SEL_FEW_EVICTED - 1]) {  // replace the largest, then bubble it into place
-            fk[SEL_FEW_EVICTED - 1] = key;
-            fc = (fc & 0x00ffffffu) | (uint32_t(k0 + u) << 24);
-#pragma unroll
-            for (int i = SEL_FEW_EVICTED - 1; i > 0; --i) {
-              if (fk[i] < fk[i - 1]) {
-                const uint64_t tk = fk[i];
-                fk[i] = fk[i - 1];
-                fk[i - 1] = tk;
-                const uint32_t hi8 = (fc >> (8 * i)) & 0xffu, lo8 = (fc >> (8 * (i - 1))) & 0xffu;
-                fc = (fc & ~(0xffffu << (8 * (i - 1)))) | (hi8 << (8 * (i - 1))) | (lo8 << (8 * i));
-              }
-            }
-          }
+          fkk = key < fmin ? k0 + u : fkk;
+          fmin = key < fmin ? key : fmin;
         }
         nprot += prot;
         nlow += prot && pb[u] < a.tail_from;
@@ -879,18 +864,47 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
   const bool few = k > 0 && !take_all && table_scores && M - k <= SEL_FEW_EVICTED;
   if (few) {
     // Few evictions (one per boundary when a row evicts at every step): the e = M - k smallest
-    // composites (hi, position), one per round, by a workgroup minimum over the threads' next
-    // candidates (a thread holds its SEL_FEW_EVICTED smallest, so it holds all of its columns
-    // among the e smallest). Each round's column leaves the kept flags. The kept set is then
-    // every composite above the e-th: the threshold (hi, 0, position + 1), every digit fixed.
+    // composites (hi, position), one per round, each the smallest above the one before, by a
+    // workgroup minimum over the threads' candidates: in round 0 the minimum phase 1 kept, later
+    // a scan of the thread's keys that reads a position only where the hi key ties. Each round's
+    // column leaves the kept flags. The kept set is then every composite above the e-th: the
+    // threshold (hi, 0, position + 1), every digit fixed.
     uint32_t ph = 0;
     int32_t pp = -1;
-    int next = 0;  // the thread's next candidate
     for (int round = 0; round < M - k; ++round) {
-      uint64_t mine = ~0ull;
-#pragma unroll
-      for (int i = 0; i < SEL_FEW_EVICTED; ++i) mine = i == next ? fk[i] : mine;
-      const int mc = next < SEL_FEW_EVICTED ? col(int((fc >> (8 * next)) & 0xffu)) : -1;
+      uint64_t mine = fmin;
+      int mc = fmin != ~0ull ? col(fkk) : -1;
+      if (round > 0) {
+        uint32_t bh = 0xffffffffu;
+        int bc = -1;
+        int32_t bp = -1;  // position of bc, read when a tie needs it
+        for (int kk = 0; kk < KPT; ++kk) {
+          const int c = col(kk);
+          if (c >= N) break;
+          const uint32_t hi = keys[c];
+          if (hi == 0 || hi < ph) continue;  // protected, or at most the previous
+          int32_t p = -1;
+          if (hi == ph) {
+            p = col_pos(a, lg, c);
+            if (p <= pp) continue;
+          }
+          if (hi < bh) {
+            bh = hi;
+            bc = c;
+            bp = p;
+          } else if (hi == bh) {
+            if (bp < 0) bp = col_pos(a, lg, bc);
+            if (p < 0) p = col_pos(a, lg, c);
+            if (p < bp) {
+              bc = c;
+              bp = p;
+            }
+          }
+        }
+        if (bc >= 0 && bp < 0) bp = col_pos(a, lg, bc);
+        mine = bc >= 0 ? (uint64_t(bh) << 32) | uint32_t(bp) : ~0ull;
+        mc = bc;
+      }
       uint64_t best = mine;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -908,10 +922,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
         const uint64_t y = (uint64_t(redu[0][w]) << 32) | redu[1][w];
         best = y < best ? y : best;
       }
-      if (mine == best && best != ~0ull) {  // positions are distinct: exactly one thread matches
-        atomicAnd(&kbits[mc >> 5], ~(1u << (mc & 31)));
-        ++next;
-      }
+      if (mine == best && best != ~0ull) atomicAnd(&kbits[mc >> 5], ~(1u << (mc & 31)));  // one thread: positions differ
       ph = uint32_t(best >> 32);
       pp = int32_t(uint32_t(best));
     }

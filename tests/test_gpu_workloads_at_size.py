@@ -196,11 +196,13 @@ def test_eviction_every_step_at_the_stress_shape(ge):
     assert ties > 0, "no exact score ties among the rows' candidates"
 
 
-@pytest.mark.parametrize("extra", [2048, 6000])
+@pytest.mark.parametrize("extra", [1, 2, 4, 2048, 6000])
 def test_selection_with_ties_at_the_cut_on_32k_rows(ge, extra):
     """Budget 32,768 (512 + 1024 + the rest scored) over 32,768 + extra candidates with 4 score
     levels: thousands of exactly tied scores straddle the cut, which the newer position wins.
-    34,816 candidates keep the selection's keys in LDS; 38,768 take the larger-row path."""
+    34,816 candidates keep the selection's keys in LDS; 38,768 take the larger-row path; 1, 2
+    and 4 evictions take the few-evictions rounds (the first from each thread's phase-1 minimum,
+    the later ones by scans that break hi-key ties by position)."""
     budget, n = 32768, 32768 + extra
     slots = n + 64
     g = torch.Generator().manual_seed(extra)
