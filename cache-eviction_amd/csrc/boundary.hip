@@ -1114,8 +1114,8 @@ __global__ void prep_slots_kernel(BndBatch b) {
 // protected columns below the tail region (Q of them, by position), the width
 // targets, then the remaining protected columns (Q = P for the reference's policies).
 // One workgroup per batch row.
-__global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndBatch b) {
-  const BndArgs a = bnd_args(b.c, b.r[blockIdx.x]);
+GSE_DEVICE void columns_row(const BndBatch& b, int row_index) {
+  const BndArgs a = bnd_args(b.c, b.r[row_index]);
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   int* tmp = reinterpret_cast<int*>(lds);
   int* bc = tmp + 128;
@@ -1624,35 +1624,72 @@ __global__ __launch_bounds__(COOP_THREADS) void relocate_coop_kernel(BndArgs a) 
   }
 }
 
-// pos_new[l, g, i'] = pos(l, g, prot_cols[i]) for the protected columns of every head row, at
-// the table's layout: i' = i below Q, width + i past it.
-// Grid (layers * kv_heads, batch rows).
-__global__ __launch_bounds__(256) void protected_pos_kernel(BndBatch b) {
-  const BndArgs a = bnd_args(b.c, b.r[blockIdx.y]);
-  const gse_boundary_status st = *a.status;
-  if (st.state != GSE_BOUNDARY_EVICTED) return;
-  const int lg = blockIdx.x;
+// pos_new[l, g, i'] = pos(l, g, prot_cols[i]) for the protected columns of head row lg, at the
+// table's layout: i' = i below Q, width + i past it. It runs beside the row's column split
+// (columns_row), so it derives the outcome that workgroup records in the row's status: the row
+// evicts when every head protects the same count P and P fits the budget.
+GSE_DEVICE void protected_pos_row(const BndBatch& b, int lg, int row_index, int* tmp) {
+  const BndArgs a = bnd_args(b.c, b.r[row_index]);
+  const int LG = a.layers * a.kv_heads;
+  int mn = INT32_MAX, mx = INT32_MIN;
+  for (int i = threadIdx.x; i < LG; i += blockDim.x) {
+    const int v = a.prot_count[i];
+    mn = min(mn, v);
+    mx = max(mx, v);
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    mn = min(mn, __shfl_xor(mn, o, 64));
+    mx = max(mx, __shfl_xor(mx, o, 64));
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    tmp[wave] = mn;
+    tmp[64 + wave] = mx;
+  }
+  __syncthreads();
+  for (int w = 0; w < int(blockDim.x >> 6); ++w) {
+    mn = min(mn, tmp[w]);
+    mx = max(mx, tmp[64 + w]);
+  }
+  const int P = a.prot_count[0];
+  if (mn != mx || P > a.budget) return;  // not evicted: the column split records why
+  const int64_t width = kept_width(a.budget, P, a.block, a.prefix_sliding);
   const int Q = a.prot_low[0];
   constexpr int B = 8;  // protected columns per thread whose loads issue together
-  const int P = st.protected_count;
-  for (int i0 = 0; i0 < P; i0 += 256 * B) {
+  const int nt = int(blockDim.x);
+  for (int i0 = 0; i0 < P; i0 += nt * B) {
     int64_t c[B];
     int32_t old[B];
 #pragma unroll
     for (int k = 0; k < B; ++k) {
-      const int i = i0 + k * 256 + int(threadIdx.x);
+      const int i = i0 + k * nt + int(threadIdx.x);
       c[k] = i < P ? a.prot_cols[i] : 0;
     }
 #pragma unroll
     for (int k = 0; k < B; ++k) old[k] = c[k] < a.row_count ? a.pos_old[int64_t(lg) * a.pstride + c[k]] : 0;
 #pragma unroll
     for (int k = 0; k < B; ++k) {
-      const int i = i0 + k * 256 + int(threadIdx.x);
+      const int i = i0 + k * nt + int(threadIdx.x);
       if (i >= P) continue;
       const int64_t p = c[k] < a.row_count ? int64_t(old[k]) : a.row_frontier + c[k] - a.row_count;
-      a.pos_new[int64_t(lg) * a.budget + (i < Q ? i : st.width + i)] = int32_t(p);
+      a.pos_new[int64_t(lg) * a.budget + (i < Q ? i : width + i)] = int32_t(p);
     }
   }
+}
+
+// The column split of every batch row (workgroups 0 .. nrows - 1) and the protected positions of
+// every (row, head row) (the workgroups after them), in one launch: they read the selection's
+// outputs only. Grid (nrows + nrows * layers * kv_heads), SEL_THREADS threads.
+__global__ __launch_bounds__(SEL_THREADS) void columns_kernel(BndBatch b) {
+  if (int(blockIdx.x) < b.nrows) {
+    columns_row(b, int(blockIdx.x));
+    return;
+  }
+  __shared__ int tmp[128];
+  const int LG = b.c.layers * b.c.kv_heads;
+  const int k = int(blockIdx.x) - b.nrows;
+  protected_pos_row(b, k % LG, k / LG, tmp);
 }
 
 // ----------------------------------------------------- table column scores --
@@ -1666,12 +1703,19 @@ __global__ void table_columns_kernel(BndBatch b) {
   const BndRow& r = b.r[blockIdx.z];
   const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const int l = blockIdx.y;
-  if (c >= r.N) return;
   const RowLayout L = row_layout(b.c, r);
-  const int32_t* slots = reinterpret_cast<const int32_t*>(r.ws + L.slots);
+  // prep_slots_kernel's work, done here for the table policies: the barrier counters and the
+  // row's slot list (layer 0's workgroups write it).
+  uint32_t* arrivals = reinterpret_cast<uint32_t*>(r.ws + L.arrivals);
+  if (c == 0 && l == 0)
+    for (int k = 0; k <= COOP_GROUPS + 1; ++k) arrivals[64 * k] = 0;  // top, group and done counters
+  if (c >= r.N) return;
+  const int32_t slot = c < r.count ? b.c.table[int64_t(r.row) * b.c.table_stride + c]
+                                   : b.c.r2t[int64_t(r.row) * b.c.r2t_stride + r.frontier + c - r.count];
+  if (l == 0) reinterpret_cast<int32_t*>(r.ws + L.slots)[c] = slot;
   float* out = reinterpret_cast<float*>(r.ws + L.col32);
   const int kv_heads = b.c.kv_heads;
-  const float* row = b.c.scores + int64_t(l) * b.c.ssl + int64_t(slots[c]) * b.c.sss;
+  const float* row = b.c.scores + int64_t(l) * b.c.ssl + int64_t(slot) * b.c.sss;
   float* col = out + int64_t(l) * kv_heads * r.N + c;
   if (kv_heads == 8 && b.c.ssg == 1 && b.c.sss == 8 && (reinterpret_cast<uintptr_t>(b.c.scores) & 15) == 0) {
     // The runtime's layout: a slot's 8 head scores are one aligned 32-byte row, two 16-byte loads.
@@ -2091,8 +2135,10 @@ int boundary_launch(const BndCommon& c, const BndRow* rows, int nrows, int coop_
     max_col_words = std::max<int64_t>(max_col_words, (rows[i].N + 31) / 32);
   }
   const unsigned col_blocks = unsigned((max_n_cols + 255) / 256);
-  hipLaunchKernelGGL(prep_slots_kernel, dim3(col_blocks, unsigned(nrows)), dim3(256), 0, s, b);
-  if (int rc = gse_launch_check("boundary prep")) return rc;
+  if (!table_policy(c.policy) || block_policy(c.policy)) {  // the table policies' column pass does it
+    hipLaunchKernelGGL(prep_slots_kernel, dim3(col_blocks, unsigned(nrows)), dim3(256), 0, s, b);
+    if (int rc = gse_launch_check("boundary prep")) return rc;
+  }
   if (block_policy(c.policy)) {
     for (int i = 0; i < nrows; ++i)
       if (int rc = block_scores(c, rows[i], s)) return rc;
@@ -2121,12 +2167,11 @@ int boundary_launch(const BndCommon& c, const BndRow* rows, int nrows, int coop_
   }
   (void)max_words;
   const size_t col_lds = size_t(128 + 16) * 4 + size_t(max_col_words) * 4 + 16;
-  hipLaunchKernelGGL(columns_kernel, dim3(unsigned(nrows)), dim3(SEL_THREADS), col_lds, s, b);
+  hipLaunchKernelGGL(columns_kernel, dim3(unsigned(nrows + nrows * LG)), dim3(SEL_THREADS), col_lds, s, b);
   if (int rc = gse_launch_check("boundary columns")) return rc;
   for (int i = 0; i < nrows; ++i)
     if (int rc = relocate_row(c, rows[i], coop_blocks, coop_per, s)) return rc;
-  hipLaunchKernelGGL(protected_pos_kernel, dim3(unsigned(LG), unsigned(nrows)), dim3(256), 0, s, b);
-  return gse_launch_check("boundary protected pos");
+  return GSE_OK;
 }
 
 int boundary_impl(void* const* k_pools, void* const* v_pools, int layers, int64_t kv_stride_s, int64_t kv_stride_h,

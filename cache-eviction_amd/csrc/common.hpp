@@ -123,9 +123,9 @@ constexpr int BUFFER_NT = 2;  // cache policy: nontemporal
 
 // 16 bytes at record `index`, byte `offset` of a structured buffer (the LLVM intrinsic; clang has
 // builtins for the raw forms only).
-GSE_DEVICE u32x4_t struct_buffer_load_b128(__amdgpu_buffer_rsrc_t rsrc, int index, int offset, int soffset,
+__device__ u32x4_t struct_buffer_load_b128(__amdgpu_buffer_rsrc_t rsrc, int index, int offset, int soffset,
                                            int aux) __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
-GSE_DEVICE void struct_buffer_store_b128(u32x4_t v, __amdgpu_buffer_rsrc_t rsrc, int index, int offset,
+__device__ void struct_buffer_store_b128(u32x4_t v, __amdgpu_buffer_rsrc_t rsrc, int index, int offset,
                                          int soffset, int aux) __asm("llvm.amdgcn.struct.ptr.buffer.store.v4i32");
 GSE_DEVICE uint4 buffer_load16_nt(__amdgpu_buffer_rsrc_t rsrc, int index, int offset) {
   return __builtin_bit_cast(uint4, struct_buffer_load_b128(rsrc, index, offset, 0, BUFFER_NT));
