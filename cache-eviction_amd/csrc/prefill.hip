@@ -165,7 +165,6 @@ template <int PASS, bool MAX_MODE>
 __global__ __launch_bounds__(64 * pf::waves<PASS>()) void prefill_kernel(PrefillArgs a) {
   using namespace pf;
   constexpr int RB = rows_per_wave<PASS>();
-  constexpr int WAVES = waves<PASS>();
   __shared__ __attribute__((aligned(16))) uint16_t ktile[2][KT * KROW];
   __shared__ float ring[PASS == 2 ? RING * KT : 1];
   const int lane = threadIdx.x & 63;
