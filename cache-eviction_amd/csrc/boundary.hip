@@ -172,6 +172,24 @@ GSE_DEVICE bool is_protected(const SelArgs& a, int64_t p) {
   return is_protected_pos(a, first) || is_protected_pos(a, first + a.block - 1);
 }
 
+// Token-granular protection covers the positions [0, pre) and [lo, n) (pre = min(prefix, n), lo
+// = min(n - recent, cursor) clamped to [0, n)). When every one of them is some column's position
+// (the protected count equals the set's size) a protected position's rank by position is
+// arithmetic: p below pre, else pre + p - lo.
+struct ProtRanks {
+  int32_t pre, lo, size;  // positions are int32
+};
+GSE_DEVICE ProtRanks prot_ranks(const SelArgs& a) {
+  const int64_t n = a.n;
+  int64_t lo = n - a.recent;
+  if (a.has_cursor && a.cursor < lo) lo = a.cursor;
+  lo = lo < 0 ? 0 : (lo > n ? n : lo);
+  const int64_t pre = a.prefix < n ? a.prefix : n;
+  return pre >= lo ? ProtRanks{int32_t(n), int32_t(n), int32_t(n)}
+                   : ProtRanks{int32_t(pre), int32_t(lo), int32_t(pre + n - lo)};
+}
+GSE_DEVICE int32_t prot_rank(const ProtRanks& r, int32_t p) { return p < r.pre ? p : r.pre + (p - r.lo); }
+
 // Kept unprotected columns: the budget left after the protected set, whole blocks only.
 GSE_DEVICE int64_t kept_width(int64_t budget, int64_t protected_count, int block, int prefix_sliding) {
   if (prefix_sliding) return 0;
@@ -750,7 +768,8 @@ GSE_DEVICE void protected_columns(const SelArgs& a, uint32_t* words, int* wpre, 
   }
 }
 
-// Grid (layers * kv_heads + 1, batch rows).
+// Grid (layers * kv_heads, batch rows): one workgroup per head row; head (0, 0)'s also ranks the
+// row's protected columns.
 __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
   const SelArgs a = select_args(b, blockIdx.y);
   constexpr int KPT = SEL_LDS_KEYS / SEL_THREADS;  // columns per thread: c = tid + k * SEL_THREADS
@@ -763,10 +782,6 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
   __shared__ uint32_t kbits[SEL_LDS_KEYS / 32];  // kept-middle flag per column
   __shared__ uint32_t redu[2][SEL_THREADS / 64];
 
-  if (int(blockIdx.x) == a.layers * a.kv_heads) {  // the extra workgroup: protected columns
-    protected_columns(a, keys, reinterpret_cast<int*>(keys + a.nwords), tmp);
-    return;
-  }
   const int lg = blockIdx.x;
   const int l = lg / a.kv_heads, g = lg % a.kv_heads;
   const int N = int(a.n_cols);
@@ -795,6 +810,11 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
   uint32_t kand = 0xffffffffu, kor = 0u;
   uint64_t fmin = ~0ull;
   int fkk = 0;
+  // Head (0, 0) ranks the row's protected columns by position (the new table's protected part):
+  // by prot_ranks where it applies, checked once the count is known, else by a bitmap pass at
+  // the end.
+  const bool prot_rank_here = lg == 0 && a.block <= 1;
+  const ProtRanks pr = prot_ranks(a);
   for (int k0 = 0; k0 < KPT; k0 += BATCH) {
     int32_t pb[BATCH];
     load_pos(k0, pb);
@@ -827,6 +847,10 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
         nprot += prot;
         nlow += prot && pb[u] < a.tail_from;
         keys[c] = hi;
+        if (prot_rank_here && prot && pb[u] < a.n) {
+          const int32_t r = prot_rank(pr, pb[u]);
+          if (uint32_t(r) < uint32_t(pr.size)) a.prot_cols[r] = c;  // the count check below decides
+        }
       }
       const uint64_t m = __ballot(unprot);
       if (lane == 0) {
@@ -1070,6 +1094,9 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
       }
     }
   }
+  if (lg != 0 || (prot_rank_here && P == pr.size)) return;
+  __syncthreads();  // every rank read of the bitmap is done: the region is reused
+  protected_columns(a, keys, reinterpret_cast<int*>(keys + a.nwords), tmp);
 }
 
 // --------------------------------------------------------- boundary kernels --
@@ -2159,7 +2186,7 @@ int boundary_launch(const BndCommon& c, const BndRow* rows, int nrows, int coop_
       }
     if (!sub.nrows) continue;
     if (pass == 0)
-      hipLaunchKernelGGL(select_row_kernel, dim3(unsigned(LG + 1), unsigned(sub.nrows)), dim3(SEL_THREADS), 0, s, sub);
+      hipLaunchKernelGGL(select_row_kernel, dim3(unsigned(LG), unsigned(sub.nrows)), dim3(SEL_THREADS), 0, s, sub);
     else
       hipLaunchKernelGGL(select_kernel<BndBatch>, dim3(unsigned(LG), unsigned(sub.nrows)), dim3(SEL_THREADS),
                          select_lds_bytes(int(words)), s, sub);
