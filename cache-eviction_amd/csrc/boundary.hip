@@ -670,34 +670,12 @@ GSE_DEVICE int cmp96(uint32_t hi, uint32_t lo, uint32_t pos, uint32_t th, uint32
   return cmp_top(pos, tp, fixed - 8);
 }
 
-// A DPP move: lane i takes `x` of the lane CTRL names (row_shr, row_bcast, wave_shl), or `old`
-// where that lane is outside the row, past the wave or in a row that ROW_MASK leaves out.
-template <int CTRL, int ROW_MASK>
-GSE_DEVICE int dpp_move(int old, int x) {
-  return __builtin_amdgcn_update_dpp(old, x, CTRL, ROW_MASK, 0xf, false);
-}
-
-// Sets bit p of the LDS bitmap for the lanes with `act` (the whole wave calls it).
+// Sets bit p of the LDS bitmap for the lanes with `act`: one LDS atomic OR per lane. Columns in
+// position order put a wave's lanes on two or three words, whose conflicting atomics the LDS
+// serialises; that measured faster than first combining each run of equal words across lanes
+// (a segmented OR scan: six dependent steps per column, by LDS permutes or by DPP moves).
 GSE_DEVICE void wave_set_bit(uint32_t* words, int32_t p, bool act) {
-  // A segmented OR in lane order: each lane gathers the bits of earlier lanes that fall in its
-  // word (an inclusive scan by doubling within each row of 16 lanes, then across rows by the
-  // row broadcasts of lanes 15 and 31, joining an earlier lane's bits only when it holds the same
-  // word), and the last lane of each run of equal words adds the run's bits with one atomic.
-  // Lanes of one run are never missed; bits joined from an earlier run of the same word are added
-  // again, which OR absorbs. Columns in position order (the common case) give one atomic per
-  // touched word. DPP moves, not LDS permutes: the chain costs a few cycles per step.
-  constexpr int NONE = -2;  // word of a lane outside the row or wave: never equal to a real one
-  const int32_t w = act ? int32_t(uint32_t(p) >> 5) : -1;
-  int v = act ? int(1u << (uint32_t(p) & 31u)) : 0;
-  auto join = [&](int y, int wy) { v = wy == w ? (v | y) : v; };
-  join(dpp_move<0x111, 0xf>(0, v), dpp_move<0x111, 0xf>(NONE, w));  // row_shr:1
-  join(dpp_move<0x112, 0xf>(0, v), dpp_move<0x112, 0xf>(NONE, w));  // row_shr:2
-  join(dpp_move<0x114, 0xf>(0, v), dpp_move<0x114, 0xf>(NONE, w));  // row_shr:4
-  join(dpp_move<0x118, 0xf>(0, v), dpp_move<0x118, 0xf>(NONE, w));  // row_shr:8
-  join(dpp_move<0x142, 0xa>(0, v), dpp_move<0x142, 0xa>(NONE, w));  // row_bcast:15 into rows 1, 3
-  join(dpp_move<0x143, 0xc>(0, v), dpp_move<0x143, 0xc>(NONE, w));  // row_bcast:31 into rows 2, 3
-  const int32_t wnext = dpp_move<0x130, 0xf>(NONE, w);               // wave_shl:1: lane + 1's word
-  if (act && wnext != w) atomicOr(&words[w], uint32_t(v));
+  if (act) atomicOr(&words[uint32_t(p) >> 5], 1u << (uint32_t(p) & 31u));
 }
 
 // wpre[w] = set bits of words[0, w) (one block scan over contiguous runs of words); the rank
