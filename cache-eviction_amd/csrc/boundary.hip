@@ -1870,18 +1870,27 @@ __global__ void swa_guard_kernel(LiveBatch b) {
     if (load_index_dyn(a.swa, a.swa_dtype, a.leftover[i]) != 0) atomicExch(&a.status->state, GSE_BOUNDARY_ERR_SWA);
 }
 
-// Grid (256, batch rows).
-__global__ void zero_leftover_kernel(LiveBatch b) {
-  const LiveArgs a = live_args(b, blockIdx.y);
-  if (a.status->state != GSE_BOUNDARY_EVICTED) return;
+// The freed slots' scores of row `row_index` become 0, by `parts` workgroups (this is part `part`).
+GSE_DEVICE void zero_leftover_row(const LiveBatch& b, int row_index, int part, int parts) {
+  const LiveArgs a = live_args(b, row_index);
+  // The row's repack runs beside this and may mark the row ERR_PACKED at any time; the scores
+  // are zeroed either way (as before the repack), and not for a row that never evicted or whose
+  // SWA guard failed.
+  const int32_t state = __hip_atomic_load(&a.status->state, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (state != GSE_BOUNDARY_EVICTED && state != GSE_BOUNDARY_ERR_PACKED) return;
   const int64_t nl = a.status->leftover;
   const int64_t total = nl * a.layers * a.kv_heads;
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+  const int64_t stride = int64_t(parts) * blockDim.x;
+  for (int64_t i = int64_t(part) * blockDim.x + threadIdx.x; i < total; i += stride) {
     const int64_t s = a.leftover[i % nl];
     const int64_t lg = i / nl;
     a.scores[(lg / a.kv_heads) * a.ssl + (lg % a.kv_heads) * a.ssg + s * a.sss] = 0.f;
   }
 }
+
+// Workgroups zeroing one row's freed scores beside its repack (the repack launch's extra
+// workgroups: a row's repack and its zeroing touch different memory).
+constexpr int ZERO_PARTS = 31;
 
 GSE_DEVICE uint32_t bitmap_load(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 GSE_DEVICE void bitmap_clear(uint32_t* p) { __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -1891,12 +1900,18 @@ GSE_DEVICE void bitmap_clear(uint32_t* p) { __hip_atomic_store(p, 0u, __ATOMIC_R
 // the caller's workspace.
 constexpr int64_t REPACK_LDS_WORDS = 36864;
 
-// One workgroup per batch row.
+// Grid (batch rows * (1 + ZERO_PARTS)): workgroup i < rows repacks row i, the others zero the
+// rows' freed scores (zero_leftover_row).
 template <bool LDS_BITMAP>
 __global__ __launch_bounds__(SEL_THREADS) void repack_kernel(LiveBatch b) {
-  const LiveArgs a = live_args(b, blockIdx.x);
   __shared__ int tmp[128 + 16];
   __shared__ uint32_t lbits[LDS_BITMAP ? REPACK_LDS_WORDS : 1];
+  if (int(blockIdx.x) >= b.nrows) {
+    const int k = int(blockIdx.x) - b.nrows;
+    zero_leftover_row(b, k % b.nrows, k / b.nrows, ZERO_PARTS);
+    return;
+  }
+  const LiveArgs a = live_args(b, blockIdx.x);
   if (a.status->state != GSE_BOUNDARY_EVICTED) return;
   const int64_t cnt = a.status->count;
   const int64_t nw = (a.num_slots + 31) >> 5;
@@ -2315,12 +2330,11 @@ int live_impl(float* scores, int layers, int64_t scores_stride_l, int kv_heads, 
       hipLaunchKernelGGL(swa_guard_kernel, dim3(64, nb), dim3(256), 0, s, b);
       if (int rc = gse_launch_check("swa guard")) return rc;
     }
-    hipLaunchKernelGGL(zero_leftover_kernel, dim3(256, nb), dim3(256), 0, s, b);
-    if (int rc = gse_launch_check("zero leftover")) return rc;
+    const dim3 grid(nb * (1 + ZERO_PARTS));
     if ((num_slots + 31) / 32 <= REPACK_LDS_WORDS)
-      hipLaunchKernelGGL(repack_kernel<true>, dim3(nb), dim3(SEL_THREADS), 0, s, b);
+      hipLaunchKernelGGL(repack_kernel<true>, grid, dim3(SEL_THREADS), 0, s, b);
     else
-      hipLaunchKernelGGL(repack_kernel<false>, dim3(nb), dim3(SEL_THREADS), 0, s, b);
+      hipLaunchKernelGGL(repack_kernel<false>, grid, dim3(SEL_THREADS), 0, s, b);
     if (int rc = gse_launch_check("repack")) return rc;
   }
   return GSE_OK;
