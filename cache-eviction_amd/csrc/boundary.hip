@@ -1043,24 +1043,30 @@ __global__ __launch_bounds__(SEL_THREADS) void select_row_kernel(BndBatch b) {
   // prefix counts in the keys region, which is free now).
   uint32_t* words = keys;
   int* wpre = reinterpret_cast<int*>(keys + a.nwords);
-  for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
-  __syncthreads();
-#pragma unroll 1
-  for (int k0 = 0; k0 < KPT; k0 += BATCH) {
+  {
+    // The first batch of positions is read while the bitmap is cleared.
     int32_t pb[BATCH];
-    load_pos(k0, pb);
+    load_pos(0, pb);
+    for (int i = threadIdx.x; i < a.nwords; i += SEL_THREADS) words[i] = 0;
+    __syncthreads();
+#pragma unroll 1
+    for (int k0 = 0; k0 < KPT; k0 += BATCH) {
+      if (k0 > 0) load_pos(k0, pb);
 #pragma unroll
-    for (int u = 0; u < BATCH; ++u) {
-      const int c = col(k0 + u);
-      wave_set_bit(words, pb[u], c < N && (kbits[c >> 5] >> (c & 31) & 1u) && pb[u] < a.n);
+      for (int u = 0; u < BATCH; ++u) {
+        const int c = col(k0 + u);
+        wave_set_bit(words, pb[u], c < N && (kbits[c >> 5] >> (c & 31) & 1u) && pb[u] < a.n);
+      }
     }
   }
+  // The rank pass's first batch of positions is read while the word prefix is formed.
+  int32_t pb[BATCH];
+  load_pos(0, pb);
   __syncthreads();
   bitmap_word_prefix(words, a.nwords, wpre, tmp);
 #pragma unroll 1
   for (int k0 = 0; k0 < KPT; k0 += BATCH) {
-    int32_t pb[BATCH];
-    load_pos(k0, pb);
+    if (k0 > 0) load_pos(k0, pb);
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
       const int c = col(k0 + u);
