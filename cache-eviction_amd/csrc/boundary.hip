@@ -699,8 +699,10 @@ GSE_DEVICE int word_rank(const uint32_t* words, const int* wpre, int32_t p) {
   return wpre[w] + __popc(words[w] & ((1u << (p & 31)) - 1u));
 }
 
-// The protected columns of head (0, 0) ranked by position (the new table's protected part),
-// by one extra workgroup of the selection grid, beside the per-head selections.
+// The protected columns of head (0, 0) ranked by position (the new table's protected part)
+// through the position bitmap: run by head (0, 0)'s workgroup at its end when the arithmetic
+// ranks of its first pass do not apply (block protection, or a protected count that differs
+// from the token-granular set's size).
 GSE_DEVICE void protected_columns(const SelArgs& a, uint32_t* words, int* wpre, int* tmp) {
   constexpr int KPT = SEL_LDS_KEYS / SEL_THREADS;
   constexpr int BATCH = 17;
