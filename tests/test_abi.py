@@ -52,6 +52,17 @@ def test_library_exports_every_declared_symbol():
     assert _native.lib().gse_version() >= 100
 
 
+def test_a_missing_library_raises_instead_of_falling_back(monkeypatch, tmp_path):
+    """With no built library every entry point raises NativeError: there is no host path to
+    fall back on."""
+    monkeypatch.setattr(_native, "LIB_PATH", str(tmp_path / "libgstar_evict.so"))
+    monkeypatch.setattr(_native, "_lib", None)
+    with pytest.raises(_native.NativeError, match="missing"):
+        _native.lib()
+    with pytest.raises(_native.NativeError, match="missing"):
+        _native.call("gse_decode")
+
+
 def test_entry_points_reject_bad_arguments_without_a_gpu():
     """Argument validation runs on the host before any launch."""
     if not os.path.exists(_native.LIB_PATH):
